@@ -1,0 +1,200 @@
+"""Benchmark of the gfx950 D64 BF16 FMHA forward (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Metric: forward TFLOP/s (repo FLOP convention 4*B*H*Sq*Sk*D, x0.5 when
+causal; reference src/bench_fmha_fwd.cpp:225-226) and its fraction of the
+MI355X dense BF16 MFMA peak (2516.6 TFLOP/s).  ``value`` is measured on the
+dense B4 H16 S2048 configuration; the causal B1 H16 S8192 (+LSE)
+configuration is reported under ``also``.  A step is one launch of the
+forward over the whole batch with Q/K/V already resident in HBM.  Inputs are
+synthetic N(0,1) bf16 (seed 42).
+
+The CPU baseline is the reference-faithful CPU oracle (oracle/, the
+restatement of src/runner/cpu_ref.cpp) timed on this host on a bounded
+row sample of the same workload.  Only this leg touches oracle/.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense BF16 FLOP/clk/CU
+HBM_PEAK_GBS = 8000.0
+
+
+def _problems():
+    from fmha_native_amd.problem import Problem
+
+    cfg2 = Problem(batch=4, nhead_q=16, seqlen_q=2048, name="cfg2")
+    cfg3 = Problem(batch=1, nhead_q=16, seqlen_q=8192, causal=True, lse=True, name="cfg3")
+    return cfg2, cfg3
+
+
+def _device_inputs(prob, torch, seed=42):
+    import numpy as np
+
+    import fmha_native_amd as fmha
+
+    nq, nk, nlse = prob.sizes()
+    host = (fmha.fill_normal(seed, nq), fmha.fill_normal(seed + 1, nk), fmha.fill_normal(seed + 2, nk))
+    dev = [torch.from_numpy(a.view(np.int16)).to("cuda:0") for a in host]
+    o = torch.empty(nq, dtype=torch.int16, device="cuda:0")
+    lse = torch.empty(nlse, dtype=torch.float32, device="cuda:0") if prob.lse else None
+    return host, dev, o, lse
+
+
+def _params(prob, dq, dk, dv, do, dlse):
+    import fmha_native_amd as fmha
+
+    p = fmha.FmhaFwdParams()
+    p.q, p.k, p.v, p.o = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), do.data_ptr()
+    p.lse = dlse.data_ptr() if dlse is not None else None
+    p.seqlen_q, p.seqlen_k, p.nhead_q, p.nhead_k = prob.seqlen_q, prob.seqlen_k, prob.nhead_q, prob.nhead_k
+    p.scale = fmha.LOG2E / math.sqrt(64.0)
+    st = prob.strides()
+    for t in "qkvo":
+        s, hs, bs = st[t]
+        setattr(p, f"stride_{t}", s)
+        setattr(p, f"nhead_stride_{t}", hs)
+        setattr(p, f"batch_stride_{t}", bs)
+    return p
+
+
+def time_problem(prob, steps, warmup, torch):
+    """Warm up, then time exactly `steps` back-to-back launches on torch's
+    current stream with HIP events recorded on that same stream."""
+    import fmha_native_amd as fmha
+
+    host, (dq, dk, dv), do, dlse = _device_inputs(prob, torch)
+    p = _params(prob, dq, dk, dv, do, dlse)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    for _ in range(warmup):
+        fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), sh)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), sh)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "host": host}
+
+
+def cpu_baseline(prob, host, budget_s=10.0):
+    """Reference-faithful oracle on rows [0, R) of every (batch, head)."""
+    import oracle
+
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    nthreads = max(1, min(nthreads, prob.batch * prob.nhead_q))  # reference parallelises over (b, h)
+    q, k, v = host
+
+    def run(rows):
+        t0 = time.perf_counter()
+        oracle.run(prob, q, k, v, faithful=True, nthreads=nthreads, rows=(0, rows))
+        return time.perf_counter() - t0
+
+    rows = 16
+    t = run(rows)
+    while t < 0.5 * budget_s and rows < prob.seqlen_q:  # grow the sample to ~budget_s
+        rows = int(min(prob.seqlen_q, max(rows + 1, rows * 0.9 * budget_s / max(t, 1e-3))))
+        t = run(rows)
+    flops = 4.0 * 64 * prob.seqlen_k * rows * prob.batch * prob.nhead_q
+    return {
+        "value": flops / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"faithful C oracle, query rows [0,{rows}) of all {prob.batch * prob.nhead_q} (b,h) of "
+                  f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q} (full keys), {t:.1f} s on {nthreads} threads",
+    }
+
+
+def _traffic():
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards "
+              "over independent (batch, head) units with no communication, so N GPUs = N independent runs",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import fmha_native_amd as fmha
+
+    fmha.load_library()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    cfg2, cfg3 = _problems()
+    r2 = time_problem(cfg2, args.steps, args.warmup, torch)
+    r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg2, r2["host"])
+
+    achieved = r2["tflops"]
+    line = {
+        "metric": "fwd TFLOP/s + % BF16 MFMA peak, d64 B4H16S2048 dense & B1H16S8192 causal",
+        "value": round(achieved, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r2["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(achieved / 348.4, 3),
+        "vs_baseline_note": "ratio to the reference's published MI300X figure for this config (348.4 TFLOP/s, "
+                            "README.md:91); no MI355X figure is published",
+        "pct_bf16_peak": round(100.0 * achieved / PEAK_BF16_TFLOPS, 2),
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V i.i.d. N(0,1) bf16, seed 42 (fill_normal)",
+        "config": {"workload": "dense MHA forward B4 H16 Sq=Sk=2048 D64, no mask, no LSE, BHSD",
+                   "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False, "lse": False},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": _traffic(),
+        },
+        "also": {
+            "workload": "causal MHA forward B1 H16 Sq=Sk=8192 D64 with LSE (FLOPs x0.5)",
+            "ms_per_step": round(r3["ms"], 5),
+            "value": round(r3["tflops"], 2),
+            "pct_bf16_peak": round(100.0 * r3["tflops"] / PEAK_BF16_TFLOPS, 2),
+            "vs_reference_mi300x": round(r3["tflops"] / 358.1, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

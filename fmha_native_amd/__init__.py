@@ -1,0 +1,194 @@
+"""fmha_native_amd — MI355X (gfx950) D64 BF16 fused multi-head attention forward.
+
+Host-side mirror of the reference's interface for this path:
+
+* ``FmhaFwdParams`` — the kernarg struct, field for field and byte for byte
+  (reference ``src/runner/params.hpp:18-64``; C declaration in
+  ``include/fmha_fwd.h``).
+* ``fmha_fwd_d64_bf16(params, batch, causal, stream)`` — the C-ABI launcher
+  that replaces the reference's launch sites (``src/bench_fmha_fwd.cpp:174-191``).
+  Errors raise :class:`FmhaError` carrying the ``hipError_t`` code.
+* ``fill_ref`` / ``fill_normal`` / ``varlen_lengths`` — the seeded input
+  generators (reference ``src/runner/buffers.cpp:99-127`` plus N(0,1)).
+* ``fmha_fwd(q, k, v, ...)`` — convenience wrapper over torch device tensors
+  (torch is used only for device memory and the stream).
+
+The compiled library ``libfmha_native_amd.so`` is required: there is no CPU or
+PyTorch fallback for the attention itself, and a missing library raises.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+
+__all__ = [
+    "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
+    "tile_config", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
+    "LOG2E", "HIP_ERROR_INVALID_VALUE",
+]
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libfmha_native_amd.so")
+LOG2E = 1.4426950408889634
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+HEAD_DIM = 64
+
+
+class FmhaError(RuntimeError):
+    """A non-zero hipError_t returned by the library."""
+
+    def __init__(self, code, what="fmha_fwd_d64_bf16"):
+        super().__init__(f"{what} returned hipError_t {code}")
+        self.code = code
+
+
+class FmhaFwdParams(ctypes.Structure):
+    """Kernarg block; identical layout to the C struct (128 bytes, align 8)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("seqlen_q", ctypes.c_int), ("seqlen_k", ctypes.c_int),
+        ("nhead_q", ctypes.c_int), ("nhead_k", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("stride_q", ctypes.c_int), ("nhead_stride_q", ctypes.c_int), ("batch_stride_q", ctypes.c_int),
+        ("stride_k", ctypes.c_int), ("nhead_stride_k", ctypes.c_int), ("batch_stride_k", ctypes.c_int),
+        ("stride_v", ctypes.c_int), ("nhead_stride_v", ctypes.c_int), ("batch_stride_v", ctypes.c_int),
+        ("stride_o", ctypes.c_int), ("nhead_stride_o", ctypes.c_int), ("batch_stride_o", ctypes.c_int),
+        ("seqstart_q", ctypes.c_void_p), ("seqstart_k", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Load the HIP library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `python -m fmha_native_amd.build` "
+            "(there is no fallback implementation)")
+    lib = ctypes.CDLL(path)
+    P = ctypes.POINTER(FmhaFwdParams)
+    lib.fmha_fwd_d64_bf16.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.fmha_fwd_d64_bf16.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_check.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    lib.fmha_fwd_d64_bf16_check.restype = ctypes.c_int
+    ip = ctypes.POINTER(ctypes.c_int)
+    lib.fmha_fwd_d64_bf16_tile_config.argtypes = [ip, ip, ip, ip]
+    lib.fmha_fwd_d64_bf16_tile_config.restype = None
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    lib.fmha_runner_fill_ref.argtypes = [ctypes.c_uint, u16p, ctypes.c_size_t, u16p, ctypes.c_size_t, u16p,
+                                         ctypes.c_size_t]
+    lib.fmha_runner_fill_ref.restype = None
+    lib.fmha_runner_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_float, u16p, ctypes.c_size_t]
+    lib.fmha_runner_fill_normal.restype = None
+    lib.fmha_runner_varlen_lengths.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ip]
+    lib.fmha_runner_varlen_lengths.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def fmha_fwd_d64_bf16(params, batch, causal, stream=None):
+    """Launch on ``stream`` (a hipStream_t as int, or None for the null stream)."""
+    rc = load_library().fmha_fwd_d64_bf16(ctypes.byref(params), int(batch), int(causal), stream)
+    if rc != HIP_SUCCESS:
+        raise FmhaError(rc)
+
+
+def check_params(params, batch, causal):
+    """Host-only argument check; returns the hipError_t code (0 = accepted)."""
+    return load_library().fmha_fwd_d64_bf16_check(ctypes.byref(params), int(batch), int(causal))
+
+
+def tile_config():
+    vals = [ctypes.c_int() for _ in range(4)]
+    load_library().fmha_fwd_d64_bf16_tile_config(*[ctypes.byref(v) for v in vals])
+    return {"kM0": vals[0].value, "kN0": vals[1].value, "kBlockSize": vals[2].value, "kHeadDim": vals[3].value}
+
+
+def _u16ptr(a):
+    assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def fill_ref(seed, nq, nk, nv):
+    """The reference generator: srand(seed) then Q, K, V (uint16 bf16 bits)."""
+    q, k, v = (np.empty(n, dtype=np.uint16) for n in (nq, nk, nv))
+    load_library().fmha_runner_fill_ref(seed, _u16ptr(q), nq, _u16ptr(k), nk, _u16ptr(v), nv)
+    return q, k, v
+
+
+def fill_normal(seed, n, mult=1.0):
+    """i.i.d. N(0,1)*mult as bf16 bits (stream ``seed``)."""
+    out = np.empty(n, dtype=np.uint16)
+    load_library().fmha_runner_fill_normal(seed, mult, _u16ptr(out), n)
+    return out
+
+
+def varlen_lengths(seed, n, lo, hi):
+    out = (ctypes.c_int * n)()
+    rc = load_library().fmha_runner_varlen_lengths(seed, n, lo, hi, out)
+    if rc != 0:
+        raise ValueError("bad varlen length request")
+    return list(out)
+
+
+def params_from_tensors(q, k, v, o, lse=None, seqstart_q=None, seqstart_k=None, max_seqlen_q=None,
+                        max_seqlen_k=None, scale=None):
+    """Build FmhaFwdParams from device tensors.
+
+    Dense: q/o are [B, Hq, Sq, 64] and k/v [B, Hk, Sk, 64] *views* with any
+    strides (BHSD, or BSHD permuted to that order).  Varlen: q/o are
+    [Hq, T, 64], k/v [Hk, T, 64], with int32 ``seqstart_*`` of batch+1 entries.
+    ``lse``: float32, [B, Hq, Sq] (dense) or [Hq, T] (varlen), contiguous.
+    """
+    p = FmhaFwdParams()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    p.lse = lse.data_ptr() if lse is not None else None
+    p.scale = LOG2E / math.sqrt(HEAD_DIM) if scale is None else float(scale)
+    varlen = seqstart_q is not None
+    if varlen:
+        p.nhead_q, p.nhead_k = q.shape[0], k.shape[0]
+        p.seqlen_q = int(max_seqlen_q)
+        p.seqlen_k = int(max_seqlen_k if max_seqlen_k is not None else max_seqlen_q)
+        for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+            setattr(p, f"stride_{name}", t.stride(1))
+            setattr(p, f"nhead_stride_{name}", t.stride(0))
+            setattr(p, f"batch_stride_{name}", 0)
+        p.seqstart_q, p.seqstart_k = seqstart_q.data_ptr(), seqstart_k.data_ptr()
+    else:
+        p.nhead_q, p.nhead_k = q.shape[1], k.shape[1]
+        p.seqlen_q, p.seqlen_k = q.shape[2], k.shape[2]
+        for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+            setattr(p, f"batch_stride_{name}", t.stride(0))
+            setattr(p, f"nhead_stride_{name}", t.stride(1))
+            setattr(p, f"stride_{name}", t.stride(2))
+        p.seqstart_q = p.seqstart_k = None
+    return p
+
+
+def fmha_fwd(q, k, v, causal=False, return_lse=False, seqstart_q=None, seqstart_k=None, max_seqlen_q=None,
+             max_seqlen_k=None, stream=None):
+    """Attention forward on torch bf16 device tensors; returns (o, lse or None).
+
+    Layouts as in :func:`params_from_tensors`; ``o`` is allocated with q's
+    shape (contiguous).  Runs on ``stream`` (default: torch's current stream).
+    """
+    import torch
+
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = None
+    if return_lse:
+        lse = torch.empty(q.shape[:-1], dtype=torch.float32, device=q.device)
+    p = params_from_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q, max_seqlen_k)
+    batch = (seqstart_q.numel() - 1) if seqstart_q is not None else q.shape[0]
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    fmha_fwd_d64_bf16(p, batch, 1 if causal else 0, stream)
+    return o, lse

@@ -1,0 +1,146 @@
+/*
+ * fmha_fwd.h — drop-in boundary of the MI355X (gfx950) D64 BF16 fused
+ * multi-head-attention forward path.
+ *
+ * Two ways in, both replacing what the reference exposes:
+ *
+ *  1. The kernarg struct FmhaFwdParams and the four __global__ entry points
+ *     fmha_fwd_d64_bf16_msk{0,1}[_varlen](FmhaFwdParams), launched by the
+ *     caller exactly as the reference's callers do:
+ *        hipLaunchKernelGGL(entry, dim3(nhead_q, ceil(seqlen_q / kM0), batch),
+ *                           dim3(kBlockSize), 0, stream, params);
+ *     Replaces: src/runner/params.hpp:18-86 (struct + tile constants) and
+ *     src/fused/kernel.cpp:55-99 (the four entries).  The grid contract is kept;
+ *     kM0/kBlockSize below are this build's tile sizes, and callers that read
+ *     them (src/bench_fmha_fwd.cpp:174-176) keep working unchanged.
+ *
+ *  2. A C-ABI launcher, fmha_fwd_d64_bf16(), which validates the arguments,
+ *     picks the entry (varlen <=> seqstart_q != NULL, causal flag), builds the
+ *     grid itself and returns a hipError_t instead of exiting.
+ *     Replaces: the launch lambda in src/bench_fmha_fwd.cpp:174-191 and the
+ *     identical launch blocks in tests/test_fmha_fwd_d64.cpp:563-578.
+ *
+ * Semantics (identical to the reference, src/runner/params.hpp:18-64):
+ *  - element (b,h,s,d) of a tensor lives at
+ *      b*batch_stride + h*nhead_stride + s*stride + d     (strides in elements)
+ *  - scale is PRE-MULTIPLIED by log2(e): scale = log2(e)/sqrt(64)
+ *  - lse == NULL disables the LSE output.  LSE is natural-log, fp32, one value
+ *    per query row.  Dense: lse[b*nhead_q*seqlen_q + h*seqlen_q + s].
+ *    Varlen: lse[h*(nhead_stride_q/stride_q) + seqstart_q[b] + s]
+ *    (src/fused/pipeline.hpp:408-418).
+ *  - seqstart_q/seqstart_k non-NULL select varlen ("group") mode: device int32
+ *    arrays of batch+1 prefix offsets; batch strides are ignored and
+ *    seqlen_q/seqlen_k are upper bounds used only for the grid.
+ *  - causal is bottom-right aligned: query row i attends key j iff
+ *    j <= i + (seqlen_k - seqlen_q)  (per sequence in varlen mode).
+ *    A query row with no visible key gets O = 0 and LSE = -inf.
+ *  - GQA/MQA: nhead_q % nhead_k == 0, KV head = h / (nhead_q / nhead_k).
+ *
+ * Requirements checked by the launcher (the reference checks none of them):
+ *  q,k,v,o non-NULL and 16-byte aligned; every stride a multiple of 8 elements
+ *  (16-byte rows); seqlen_* >= 0; nhead_k > 0; nhead_q % nhead_k == 0; both or
+ *  neither seqstart pointer set; every in-tensor offset of one (batch, head)
+ *  fits in 31 bits.  Violations return hipErrorInvalidValue and launch nothing.
+ */
+#ifndef FMHA_FWD_H_
+#define FMHA_FWD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#if defined(__cplusplus) && defined(__HIPCC__)
+#include <hip/hip_bf16.h>
+typedef __hip_bfloat16 fmha_bf16_t;
+#else
+typedef uint16_t fmha_bf16_t; /* bf16 bit pattern; same size and alignment */
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Kernarg block, passed by value.  Field order and offsets are the ABI and are
+ * identical to the reference's struct (src/runner/params.hpp:18-64):
+ * q@0 k@8 v@16 o@24 lse@32 seqlen_q@40 seqlen_k@44 nhead_q@48 nhead_k@52
+ * scale@56 q-strides@60 k-strides@72 v-strides@84 o-strides@96 (pad@108)
+ * seqstart_q@112 seqstart_k@120; sizeof 128, alignof 8. */
+typedef struct FmhaFwdParams {
+    const fmha_bf16_t *q, *k, *v;
+    fmha_bf16_t* o;
+    float* lse;
+    int seqlen_q, seqlen_k;
+    int nhead_q, nhead_k;
+    float scale;
+    int stride_q, nhead_stride_q, batch_stride_q;
+    int stride_k, nhead_stride_k, batch_stride_k;
+    int stride_v, nhead_stride_v, batch_stride_v;
+    int stride_o, nhead_stride_o, batch_stride_o;
+    const int32_t* seqstart_q;
+    const int32_t* seqstart_k;
+} FmhaFwdParams;
+
+/* Tile geometry (same values as the reference, params.hpp:70-86).  One block
+ * owns FMHA_KM0 query rows of one (batch, head): FMHA_KBLOCK/64 waves of 32
+ * query rows each; keys are walked in tiles of FMHA_KN0. */
+#define FMHA_KM0 128
+#define FMHA_KN0 64
+#define FMHA_KBLOCK 256
+#define FMHA_HEAD_DIM 64
+
+/* Launch the D64 BF16 forward pass on `stream`.
+ *   params : kernarg (host memory; copied by value)
+ *   batch  : number of sequences (dense batch, or number of varlen sequences)
+ *   causal : 0 = no mask (reference --mask 0), 1 = bottom-right causal (--mask 1)
+ * Returns hipSuccess, hipErrorInvalidValue for rejected arguments (nothing is
+ * launched), or the launch error.  Asynchronous like any kernel launch; it
+ * allocates nothing and keeps no state, so concurrent calls are safe.
+ * Replaces src/bench_fmha_fwd.cpp:174-191. */
+hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
+                             hipStream_t stream);
+
+/* Argument checks of fmha_fwd_d64_bf16 without launching (host only, no GPU
+ * needed).  Returns hipSuccess or hipErrorInvalidValue. */
+hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int causal);
+
+/* Tile constants of the linked library, so FFI callers (ctypes, cgo) need not
+ * parse this header: writes kM0, kN0, kBlockSize, head dim. */
+void fmha_fwd_d64_bf16_tile_config(int* m0, int* n0, int* block_size, int* head_dim);
+
+#ifdef __cplusplus
+} /* extern "C" */
+
+static_assert(sizeof(FmhaFwdParams) == 128, "FmhaFwdParams must stay 128 bytes");
+static_assert(alignof(FmhaFwdParams) == 8, "FmhaFwdParams alignment");
+static_assert(offsetof(FmhaFwdParams, lse) == 32, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, seqlen_q) == 40, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, scale) == 56, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, stride_q) == 60, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, stride_k) == 72, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, stride_v) == 84, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, stride_o) == 96, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, seqstart_q) == 112, "kernarg layout");
+static_assert(offsetof(FmhaFwdParams, seqstart_k) == 120, "kernarg layout");
+
+/* The reference's C++ tile constants, same names (src/runner/params.hpp:70-86). */
+constexpr int kM0 = FMHA_KM0;
+constexpr int kN0 = FMHA_KN0;
+constexpr int kBlockSize = FMHA_KBLOCK;
+constexpr int kHeadDim = FMHA_HEAD_DIM;
+constexpr int kWarpSize = 64;
+constexpr int kNumWarps = FMHA_KBLOCK / 64;
+
+#if defined(__HIPCC__)
+/* The four launchable entries (reference src/fused/kernel.cpp:55-99).  Grid
+ * (nhead_q, ceil(seqlen_q/kM0), batch), block kBlockSize, no dynamic LDS. */
+__global__ void fmha_fwd_d64_bf16_msk0(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_msk1(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_msk0_varlen(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_msk1_varlen(FmhaFwdParams params);
+#endif
+#endif /* __cplusplus */
+
+#endif /* FMHA_FWD_H_ */
