@@ -136,6 +136,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["cfg2", "cfg3"], help="time one workload only (profiling runs)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run `steps` device-to-device copies of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards "
@@ -149,7 +152,21 @@ def main():
 
     fmha.load_library()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": args.steps}))
+        return
     cfg2, cfg3 = _problems()
+    if args.only:
+        prob = cfg2 if args.only == "cfg2" else cfg3
+        r = time_problem(prob, args.steps, args.warmup, torch)
+        print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"]}), flush=True)
+        return
     r2 = time_problem(cfg2, args.steps, args.warmup, torch)
     r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)
 
