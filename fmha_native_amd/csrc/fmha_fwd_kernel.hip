@@ -17,20 +17,31 @@
 //    k-index for lane half h / element e is matched by reading V^T with the
 //    SAME key permutation (key = 16t + 8(e/4) + 4h + e%4), which
 //    ds_read_b64_tr_b16 delivers from a row-major [key][d] LDS tile.
-//  * K and V tiles go HBM/L2 -> LDS directly (buffer_load_dwordx4 ... lds),
-//    double-buffered with one s_barrier per tile; 16-byte chunks of each
-//    128-byte row are XOR-swizzled so the b128 (K) and tr_b16 (V) reads are
-//    bank-conflict free.  Out-of-range rows are zero-filled by the buffer
-//    descriptor's num_records bound (never read past a tensor or sequence).
+//  * In-wave software pipeline.  Iteration t issues the 16 MFMAs of
+//    GEMM1(tile t-1) and GEMM0(tile t+1) interleaved with the softmax VALU
+//    work of tile t (sched_group_barrier): the three stages have no data
+//    dependence on each other inside an iteration, so one wave keeps the
+//    matrix core and the VALU busy at the same time.
+//  * K and V tiles go HBM/L2 -> LDS directly (buffer_load_dwordx4 ... lds)
+//    in two 4-deep rings: K(t+4) and V(t+2) are fetched during iteration t,
+//    i.e. both three iterations before they are read; one s_barrier per tile.
+//    The loop is unrolled by the ring depth so every LDS stage offset is an
+//    instruction immediate.
+//    16-byte chunks of each 128-byte row are XOR-swizzled so the b128 (K)
+//    and tr_b16 (V) reads are bank-conflict free.  Out-of-range rows are
+//    zero-filled by the buffer descriptor's num_records bound (never read past
+//    a tensor or sequence).
 //  * Softmax in the exp2 domain with the log2(e) already folded into scale
-//    (as the reference, params.hpp:38-43); the running max is only moved
-//    when a tile's max exceeds it by more than 8 (log2 units), so the O^T
-//    rescale is skipped on almost every tile; P <= 2^8 is exact-range safe.
-//  * 4 waves x <=128 VGPRs so 4 blocks (16 waves) share a CU: MFMA of one
-//    wave overlaps the exp/FMA softmax of the others on the same SIMD.
+//    (as the reference, params.hpp:38-43), speculative: P is computed in the
+//    current reference-max frame without taking the tile's max; only when a
+//    lane's tile sum of P exceeds 256 (so some score is far above the frame)
+//    does the wave take the exact max, rescale O^T and l, and redo the tile.
+//    Any frame gives the same O and LSE; this one keeps every P <= 256.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <utility>
 
 #include "fmha_fwd.h"
 
@@ -49,45 +60,47 @@ constexpr int kTileM = kWaves * kRowsPerWave;  // 128
 constexpr int kTileN = FMHA_KN0;               // 64 keys per tile
 constexpr int kRowBytes = 128;                 // 64 bf16 per K/V row in LDS
 constexpr int kTileBytes = kTileN * kRowBytes; // 8 KiB
-constexpr int kStageBytes = 2 * kTileBytes;    // K + V
-constexpr int kStages = 2;
-constexpr int kLdsBytes = kStages * kStageBytes;  // 32 KiB
-constexpr float kRescaleThreshold = 8.0f;         // log2 units
-constexpr float kMaxSeed = -5000.0f;              // raw-score running max seed (pipeline.hpp:248-252)
-constexpr uint32_t kBufferWord3 = 0x00020000u;    // raw dword buffer, gfx9 family
+constexpr int kRing = 4;                       // stages per ring (K and V)
+constexpr int kLdsBytes = 2 * kRing * kTileBytes;  // 64 KiB in 2*kRing separate arrays
+constexpr int kLoadsPerTile = 2;                   // 1 KiB DMA per load, per wave
+constexpr float kGrowSum = 256.0f;                 // tile-sum bound of the speculative softmax
+constexpr float kMaxSeed = -5000.0f;               // raw-score running max seed (pipeline.hpp:248-252)
+constexpr uint32_t kBufferWord3 = 0x00020000u;     // raw dword buffer, gfx9 family
+
+// sched_group_barrier instruction classes
+constexpr int kSchedVALU = 0x002;
+constexpr int kSchedMFMA = 0x008;
+constexpr int kSchedDSRead = 0x100;
 
 static_assert(kTileM == FMHA_KM0, "tile rows must match the grid contract");
+static_assert(kWaves * kLoadsPerTile * 1024 == kTileBytes, "one tile = one DMA round of the block");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)num_bytes, (int)kBufferWord3);
 }
 
-// Same descriptor as plain dwords, for the inline-asm LDS-DMA loads.
-__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t num_bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    i32x4 w;
-    w[0] = (int)(uint32_t)a;
-    w[1] = (int)((uint32_t)(a >> 32) & 0xffffu);  // stride 0, no swizzle
-    w[2] = (int)num_bytes;
-    w[3] = (int)kBufferWord3;
-    return w;
-}
+typedef __attribute__((address_space(3))) char lds_char;
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
+// The LDS rings: every stage is its own __shared__ array, so the compiler's
+// LDS alias scopes tell its waitcnt pass that a prefetch into one stage does
+// not alias reads of the others (with one flat buffer it would wait for every
+// in-flight prefetch before each LDS read).
+struct Ring {
+    lds_char* k[kRing];
+    lds_char* v[kRing];
+};
 
-// 64 lanes x 16 bytes global -> LDS, lane L lands at lds + 16*L.  Issued as
-// inline asm so the compiler's waitcnt pass does not treat the in-flight
-// prefetch as aliasing every LDS read (it would insert vmcnt(0) before them);
-// completion is awaited explicitly with vmcnt_wait0() before the tile barrier.
-__device__ __forceinline__ void lds_dma_16(const i32x4& rsrc, uint32_t lds, int voffset) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds), "v"(voffset), "s"(rsrc)
-                 : "memory", "m0");
+// 64 lanes x 16 bytes global -> LDS (buffer_load_dwordx4 ... lds); lane L
+// lands at dst + 16*L.  dst must be wave-uniform.
+__device__ __forceinline__ void lds_dma_16(__amdgpu_buffer_rsrc_t rsrc, lds_char* dst, int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, voffset, 0, 0, 0);
 }
-__device__ __forceinline__ void vmcnt_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Own-wave DMA completion before a tile barrier (the barrier then makes every
+// wave's part of the tile visible).
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // XOR swizzle of the 16-byte chunk index inside a 128-byte K row (row & 15 is
 // all it depends on).  Conflict-free ds_read_b128 for both 32- and 64-bank LDS.
@@ -104,16 +117,58 @@ __device__ __forceinline__ float wave_sum_halves(float x) {
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-__device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
-    bf16x8 r;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (__bf16)s[base + e];
-    return r;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ bf16x8 lds_read_b128(const lds_char* p) { return *(const lds_bf16x8*)p; }
+// 8 keys x 1 head-dim column of V for the GEMM1 A operand (two tr_b16 reads,
+// rows key0..key0+3 and key0+8..key0+11).
+__device__ __forceinline__ bf16x8 lds_read_vt(const lds_char* p) {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * kRowBytes));
+    i16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
 }
+
+__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Schedule of one pipelined iteration: 16 slots of {1 MFMA, DS reads for the
+// MFMA two slots ahead, kValuPerSlot VALU}; GEMM1 MFMAs take two tr_b16
+// reads, GEMM0 MFMAs one b128 read.  Groups are filled in order, respecting
+// dependences.  The softmax of a tile is ~117 VALU (32 fma, 32 exp, 35 add,
+// 16 cvt_pk, bookkeeping), spread evenly over the 16 MFMAs.
+#ifndef FMHA_VALU_PER_SLOT
+#define FMHA_VALU_PER_SLOT 8
+#endif
+constexpr int kValuPerSlot = FMHA_VALU_PER_SLOT;
+template <int I>
+__device__ __forceinline__ void sched_slot() {
+    __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+    if constexpr (I < 6)
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+    else if constexpr (I < 14)
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVALU, kValuPerSlot, 0);
+}
+template <int... Is>
+__device__ __forceinline__ void sched_iteration(std::integer_sequence<int, Is...>) {
+    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+    (sched_slot<Is>(), ...);
+}
+
+// Online-softmax state of one lane's query row (both lane halves of a row keep
+// the same m_ref; l_part is this lane's partial sum).
+struct Softmax {
+    float m_ref;   // reference max (raw score units)
+    float l_part;  // partial row sum of P in the m_ref frame, tiles before the current one
+    float l_tile;  // this lane's sum of P over the current tile
+};
 
 // One block = one kTileM-row M-tile of (batch b, head h).
 template <bool kCausal, bool kVarlen>
-__device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, char* smem) {
+__device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, const Ring& ring) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int l32 = lane & 31;
@@ -189,10 +244,12 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
     }
 
-    // ---- global -> LDS tile loader: each wave moves 2 x 1 KiB of K and of V.
-    // Lane L of load i writes LDS row 8*(2*wave+i) + L/8, physical chunk L%8,
-    // fetched from logical chunk (L%8) ^ swz(row). ----
-    const int ld_row = (2 * wave) * 8 + (lane >> 3);  // + 8 for i = 1
+    // ---- global -> LDS tile loaders: per tile each wave moves 2 x 1 KiB of
+    // K (or V).  Lane L of load i writes LDS row 8*(2*wave+i) + L/8, physical
+    // chunk L%8, fetched from logical chunk (L%8) ^ swz(row).  Tiles past the
+    // KV range get an empty descriptor (zero fill, no memory traffic), so
+    // every iteration issues the same number of loads. ----
+    const int ld_row = (2 * wave) * 8 + (lane >> 3);
     const int ld_pc = lane & 7;
     const int k_ld_off0 = ld_row * p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row)) << 4);
     const int k_ld_off1 = (ld_row + 8) * p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row + 8)) << 4);
@@ -200,23 +257,30 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int v_ld_off1 = (ld_row + 8) * p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row + 8)) << 4);
     const int k_tile_step = kTileN * p.stride_k * 2;
     const int v_tile_step = kTileN * p.stride_v * 2;
+    const int wave_off = (2 * wave) * 1024;
 
-    const i32x4 rk_w = make_rsrc_words(kbase, kbytes);
-    const i32x4 rv_w = make_rsrc_words(vbase, vbytes);
-    const uint32_t lds_wave = lds_addr(smem) + (2 * wave) * 1024;
-    auto issue_tile = [&](int tile, int stage) {
-        const uint32_t st = lds_wave + stage * kStageBytes;
-        const int kt = tile * k_tile_step;
-        const int vt = tile * v_tile_step;
-        lds_dma_16(rk_w, st, k_ld_off0 + kt);
-        lds_dma_16(rk_w, st + 1024, k_ld_off1 + kt);
-        lds_dma_16(rv_w, st + kTileBytes, v_ld_off0 + vt);
-        lds_dma_16(rv_w, st + kTileBytes + 1024, v_ld_off1 + vt);
+    // Tile t's K lands in K stage t % kRing, its V in V stage t % kRing.  The
+    // tile's own descriptor (base at the tile's first row, num_records = bytes
+    // left; 0 for a dead tile) is built in scalar registers, so the per-lane
+    // offsets stay loop-invariant.
+    auto issue_k = [&](int tile, auto stage_c) {
+        lds_char* dst = ring.k[decltype(stage_c)::value] + wave_off;
+        const uint32_t t0 = (uint32_t)tile * (uint32_t)k_tile_step;
+        const auto r = make_rsrc((const char*)kbase + t0, tile < ntiles ? kbytes - t0 : 0u);
+        lds_dma_16(r, dst, k_ld_off0);
+        lds_dma_16(r, dst + 1024, k_ld_off1);
+    };
+    auto issue_v = [&](int tile, auto stage_c) {
+        lds_char* dst = ring.v[decltype(stage_c)::value] + wave_off;
+        const uint32_t t0 = (uint32_t)tile * (uint32_t)v_tile_step;
+        const auto r = make_rsrc((const char*)vbase + t0, tile < ntiles ? vbytes - t0 : 0u);
+        lds_dma_16(r, dst, v_ld_off0);
+        lds_dma_16(r, dst + 1024, v_ld_off1);
     };
 
-    // ---- per-lane LDS read addresses ----
+    // ---- per-lane LDS read offsets inside a tile ----
     // K (A of GEMM0): lane (i=l32, h) reads row kb*32 + i, logical chunk 2t + h.
-    int k_rd[4];
+    uint32_t k_rd[4];
     {
         const int f = k_swz(l32);
 #pragma unroll
@@ -226,7 +290,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     // lane 4e + c supplies the address of 4 d-values (d = dbase + 4c) of key
     // row key0 + e; lane i of the group then receives V[key0 + e][dbase + i]
     // for e = 0..3.  key0 = kb*32 + 16t + 8u + 4h, dbase = 32db + 16*(g%2).
-    int v_rd[2];
+    uint32_t v_rd[2];
     {
         const int g = lane >> 4, i16 = lane & 15;
         const int e = i16 >> 2, c = i16 & 3;
@@ -234,121 +298,220 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
             const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-            v_rd[db] = kTileBytes + row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
+            v_rd[db] = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
         }
     }
 
-    // ---- online-softmax state (per lane = per query row; both lane halves
-    // of a row keep identical m, partial l) ----
-    const float scale = p.scale;                       // log2(e)/sqrt(D)
-    const float thr_raw = kRescaleThreshold / scale;   // threshold in raw-score units
-    float m_ref = kMaxSeed;
-    float l_part = 0.0f;
+    const float scale = p.scale;  // log2(e)/sqrt(D)
+    Softmax sm{kMaxSeed, 0.0f, 0.0f};
+    constexpr int kBlockSize = FMHA_KBLOCK;
     f32x16 oacc[2];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
 
-    // Rows this wave can see: causal limit of its last row.
-    const int wave_key_limit = kCausal ? (wrow0 + kRowsPerWave - 1 + shift) : 0x7fffffff;
-    const bool wave_active = wrow0 < sq;
-
-    if (ntiles > 0) issue_tile(0, 0);
-
-    for (int j = 0; j < ntiles; ++j) {
-        const int stage = j & 1;
-        // own loads of tile j complete, then make everybody's visible; the same
-        // barrier also retires every wave's reads of stage (j+1)&1 (tile j-1).
-        vmcnt_wait0();
-        __syncthreads();
-        if (j + 1 < ntiles) issue_tile(j + 1, stage ^ 1);
-
-        const int key0 = j * kTileN;
-        if (!wave_active || key0 > wave_key_limit) continue;  // wave fully masked for this tile
-
-        const char* st = smem + stage * kStageBytes;
-
-        // ---- GEMM0: S^T[kb] = K[kb] . Q^T ----
-        f32x16 s[2];
+    // ---- the three pipeline stages (stage indices are compile-time) ----
+    // GEMM0 of the tile in K stage KS: S^T[kb] = K[kb] . Q^T
+    auto gemm0 = [&](auto ks_c, f32x16* s) {
+        const lds_char* st = ring.k[decltype(ks_c)::value];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             f32x16 acc = {};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bf16x8 kop = *(const bf16x8*)(st + kb * 32 * kRowBytes + k_rd[t]);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[t], acc, 0, 0, 0);
-            }
+            for (int k = 0; k < 4; ++k) acc = mfma(lds_read_b128(st + k_rd[k] + kb * 32 * kRowBytes), qop[k], acc);
             s[kb] = acc;
         }
-
-        // ---- mask: keys >= sk, and (causal) keys > row + shift ----
-        const bool need_mask = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
-        if (need_mask) {
+    };
+    // GEMM1 of the tile in V stage VS: O^T[db] += V^T[db] . P^T
+    auto gemm1 = [&](auto vs_c, const bf16x8* pp) {
+        const lds_char* st = ring.v[decltype(vs_c)::value];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    oacc[db] = mfma(lds_read_vt(st + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[2 * kb + k],
+                                    oacc[db]);
+    };
+    // mask of tile t: keys >= sk, and (causal) keys > row + shift
+    auto mask_tile = [&](int t, f32x16* s) {
+        const int key0 = t * kTileN;
+        const bool need = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
+        if (need) {
+            // element (kb, r) holds key key0 + 4h + c with c = 32kb + 8(r/4) + r%4;
+            // it is visible iff c <= d.  Bit c of the lane's 64-bit map says so;
+            // each element is then one bit extract + one bit-select.
             const int lim = kCausal ? min(sk - 1, my_row + shift) : sk - 1;
+            const int d = lim - (key0 + 4 * hi);
+            const uint32_t lo = d < 0 ? 0u : (d >= 31 ? 0xffffffffu : (2u << d) - 1u);
+            const uint32_t hi_bits = d < 32 ? 0u : (d >= 63 ? 0xffffffffu : (2u << (d - 32)) - 1u);
+            const uint32_t ninf = 0xff800000u;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = key0 + kb * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (key > lim) s[kb][r] = -INFINITY;
+                    const int c = 8 * (r >> 2) + (r & 3);
+                    const uint32_t bits = kb ? hi_bits : lo;
+                    const uint32_t m = (uint32_t)((int32_t)(bits << (31 - c)) >> 31);  // 0 or all ones
+                    s[kb][r] = __uint_as_float((__float_as_uint(s[kb][r]) & m) | (ninf & ~m));
                 }
         }
-
-        // ---- row max over the tile; move the reference max only when the
-        // tile exceeds it by > kRescaleThreshold (log2 units) ----
-        float mx = s[0][0];
+    };
+    // exact max of a score tile over the lane's row (both lane halves)
+    auto tile_max = [&](const f32x16* s) {
+        float mp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mp[i] = fmaxf(fmaxf(s[i >> 2][4 * (i & 3)], s[i >> 2][4 * (i & 3) + 1]),
+                                                  fmaxf(s[i >> 2][4 * (i & 3) + 2], s[i >> 2][4 * (i & 3) + 3]));
+        const float mx = fmaxf(fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3])),
+                               fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7])));
+        return wave_max_halves(mx);
+    };
+    // P = exp2(s*scale - m_ref*scale), bf16-packed into the GEMM1 B operands,
+    // and this lane's tile sum of P (fp32, before the bf16 rounding).
+    auto exp_tile = [&](const f32x16* s, bf16x8* pp) {
+        const float neg_ms = -sm.m_ref * scale;
+        float ls[4];  // 4 independent partial chains (latency)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        mx = wave_max_halves(mx);
-        const bool grow = mx > m_ref + thr_raw;
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float m_new = grow ? mx : m_ref;
-            const float alpha = __builtin_amdgcn_exp2f((m_ref - m_new) * scale);
-            l_part *= alpha;
+            for (int k = 0; k < 2; ++k) {
+                bf16x8 pk;
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 * k + e], scale, neg_ms));
+                    acc += pv;
+                    pk[e] = (__bf16)pv;
+                }
+                ls[2 * kb + k] = acc;
+                pp[2 * kb + k] = pk;
+            }
+        sm.l_tile = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+    // Softmax of one tile, speculatively in the current m_ref frame: no max
+    // is taken on this path.  P and its sum stay exact whatever m_ref is, as
+    // long as nothing overflows; settle() re-runs the tile with a new m_ref
+    // when the tile sum leaves the safe range.
+    auto softmax = [&](const f32x16* s, bf16x8* pp) {
+        exp_tile(s, pp);
+        // keep P and the tile sum computed in this block: both would otherwise
+        // be sunk towards their next use, out of the interleaved region
+        asm volatile("" ::"v"(pp[0]), "v"(pp[1]), "v"(pp[2]), "v"(pp[3]), "v"(sm.l_tile));
+    };
+    // After the interleaved block of tile t (whose GEMM1(t-1) has then been
+    // issued): a lane whose tile sum exceeds kGrowSum (every P <= the sum, so
+    // P <= kGrowSum otherwise) has scores well above m_ref.  Then the whole
+    // wave moves m_ref to max(m_ref, tile max), rescales O^T and l, and
+    // recomputes the tile's P.  The first tile's m_ref is set exactly before
+    // the loop, so this path is only taken when a row's max grows by more
+    // than log2(kGrowSum / 32) after its first tile.
+    auto settle = [&](const f32x16* s, bf16x8* pp) {
+        if (__builtin_amdgcn_ballot_w64(!(sm.l_tile <= kGrowSum))) {
+            asm volatile("" ::: "memory");  // a side effect: keeps the rare path a branch, not speculated
+            const float m_new = fmaxf(sm.m_ref, tile_max(s));
+            const float alpha = __builtin_amdgcn_exp2f((sm.m_ref - m_new) * scale);
+            sm.m_ref = m_new;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-            m_ref = m_new;
+            sm.l_part *= alpha;
+            exp_tile(s, pp);
         }
+        sm.l_part += sm.l_tile;
+    };
+    auto interleave = [&]() { sched_iteration(std::make_integer_sequence<int, 16>{}); };
 
-        // ---- P = exp2(s*scale - m_ref*scale), partial row sum, bf16 pack ----
-        const float neg_ms = -m_ref * scale;
-        float lsum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], scale, neg_ms));
-                s[kb][r] = pv;
-                lsum += pv;
-            }
-        l_part += lsum;
+    f32x16 sacc[2][2];  // S^T of two consecutive tiles (alternating roles)
+    bf16x8 pbuf[2][4];  // P^T of two consecutive tiles (alternating roles)
 
-        // ---- GEMM1: O^T[db] += V^T[db] . P^T ----
+    // iteration t (phase J = t % kRing): GEMM1(t-1) || GEMM0(t+1) || softmax(t)
+    auto iteration = [&](int t, auto phase_c) {
+        constexpr int J = decltype(phase_c)::value;
+        constexpr int cur = J & 1, nxt = cur ^ 1;
+        // K(t+1) and V(t-1) were fetched three iterations ago; the loads of
+        // the two previous iterations may still fly.
+        vmcnt_wait<4 * kLoadsPerTile>();
+        __syncthreads();
+        issue_k(t + kRing, std::integral_constant<int, J>{});
+        issue_v(t + 2, std::integral_constant<int, (J + 2) % kRing>{});
+        mask_tile(t, sacc[cur]);
+        gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[nxt]);
+        gemm0(std::integral_constant<int, (J + 1) % kRing>{}, sacc[nxt]);
+        softmax(sacc[cur], pbuf[cur]);
+        interleave();
+        settle(sacc[cur], pbuf[cur]);
+    };
+    // the last GEMM1, for tile t of phase J
+    auto last_gemm1 = [&](auto phase_c) {
+        constexpr int J = decltype(phase_c)::value;
+        vmcnt_wait<0>();  // every DMA landed (none may outlive the block)
+        __syncthreads();
+        gemm1(std::integral_constant<int, J>{}, pbuf[J & 1]);
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
+
+    if (ntiles > 0) {
+        // GEMM1(-1) of iteration 0 runs on P = 0 and a zeroed V stage, which
+        // contributes exactly 0 and keeps the loop body branch-free.
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const bf16x8 pop = pack8(s[kb], 8 * t);
-#pragma unroll
-                for (int db = 0; db < 2; ++db) {
-                    const int a0 = v_rd[db] + (kb * 32 + 16 * t) * kRowBytes;
-                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(st + a0));
-                    const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(st + a0 + 8 * kRowBytes));
-                    i16x4 both[2] = {lo, hi4};
-                    const bf16x8 vop = __builtin_bit_cast(bf16x8, both);
-                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, oacc[db], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) pbuf[1][i] = bf16x8{};
+        {
+            typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
+            lds_i32x4* z = (lds_i32x4*)ring.v[kRing - 1];
+            z[threadIdx.x] = i32x4{};
+            z[threadIdx.x + kBlockSize] = i32x4{};
+        }
+        // prologue: K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once K0 landed
+        issue_k(0, P0{});
+        issue_k(1, P1{});
+        issue_v(0, P0{});
+        issue_k(2, P2{});
+        issue_v(1, P1{});
+        issue_k(3, P3{});
+        vmcnt_wait<5 * kLoadsPerTile>();
+        __syncthreads();
+        gemm0(P0{}, sacc[0]);
+        // m_ref starts at the first tile's exact (masked) row max, so the
+        // speculative softmax holds from tile 0 on (rows with no visible key
+        // there keep the finite seed: their P is exactly 0)
+        mask_tile(0, sacc[0]);
+        sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]));
+        int t = 0;
+        for (; t + kRing <= ntiles; t += kRing) {
+            iteration(t, P0{});
+            iteration(t + 1, P1{});
+            iteration(t + 2, P2{});
+            iteration(t + 3, P3{});
+        }
+        const int rem = ntiles - t;
+        if (rem == 0) {
+            last_gemm1(P3{});
+        } else {
+            iteration(t, P0{});
+            if (rem == 1) {
+                last_gemm1(P0{});
+            } else {
+                iteration(t + 1, P1{});
+                if (rem == 2) {
+                    last_gemm1(P1{});
+                } else {
+                    iteration(t + 2, P2{});
+                    last_gemm1(P2{});
                 }
             }
+        }
     }
 
     // ---- epilogue: O = O^T / l (rows < sq; the buffer bound drops the rest),
     // LSE = (log2(l) + scale*m) * ln2 (natural log, -inf for an empty row) ----
-    const float l_tot = wave_sum_halves(l_part);
+    const float l_tot = wave_sum_halves(sm.l_part);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     {
         const int orow_off = my_row * p.stride_o * 2;
@@ -374,7 +537,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             lse_base = p.lse + (int64_t)h * (p.nhead_stride_q / p.stride_q) + off_q;
         else
             lse_base = p.lse + (int64_t)b * p.nhead_q * p.seqlen_q + (int64_t)h * p.seqlen_q;
-        const float lse2 = __builtin_log2f(l_tot) + m_ref * scale;  // -inf when l == 0
+        const float lse2 = __builtin_log2f(l_tot) + sm.m_ref * scale;  // -inf when l == 0
         lse_base[my_row] = lse2 * 0.69314718055994530942f;
     }
 }
@@ -386,21 +549,28 @@ using namespace fmha_gfx950;
 // ---- the four entries (reference src/fused/kernel.cpp:55-99).  Grid
 // (nhead_q, ceil(seqlen_q/kM0), batch).  Causal entries run the heaviest
 // M-tiles first (kernel.cpp:73,96). ----
-#define FMHA_ENTRY_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
+#define FMHA_ENTRY_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// eight distinct LDS arrays = the K and V ring stages
+#define FMHA_RING(r)                                                                                          \
+    __shared__ __attribute__((aligned(1024))) char r##_k0[kTileBytes], r##_k1[kTileBytes], r##_k2[kTileBytes], \
+        r##_k3[kTileBytes], r##_v0[kTileBytes], r##_v1[kTileBytes], r##_v2[kTileBytes], r##_v3[kTileBytes];   \
+    const Ring r{{(lds_char*)r##_k0, (lds_char*)r##_k1, (lds_char*)r##_k2, (lds_char*)r##_k3},                \
+                 {(lds_char*)r##_v0, (lds_char*)r##_v1, (lds_char*)r##_v2, (lds_char*)r##_v3}};
+static_assert(kRing == 4, "FMHA_RING declares four stages per ring");
 
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0(FmhaFwdParams params) {
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    fwd_mtile<false, false>(params, blockIdx.z, blockIdx.x, blockIdx.y, smem);
+    FMHA_RING(ring)
+    fwd_mtile<false, false>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1(FmhaFwdParams params) {
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    fwd_mtile<true, false>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, smem);
+    FMHA_RING(ring)
+    fwd_mtile<true, false>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0_varlen(FmhaFwdParams params) {
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    fwd_mtile<false, true>(params, blockIdx.z, blockIdx.x, blockIdx.y, smem);
+    FMHA_RING(ring)
+    fwd_mtile<false, true>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen(FmhaFwdParams params) {
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    fwd_mtile<true, true>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, smem);
+    FMHA_RING(ring)
+    fwd_mtile<true, true>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
