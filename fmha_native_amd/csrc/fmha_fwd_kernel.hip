@@ -140,7 +140,7 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 // dependences.  The softmax of a tile is ~117 VALU (32 fma, 32 exp, 35 add,
 // 16 cvt_pk, bookkeeping), spread evenly over the 16 MFMAs.
 #ifndef FMHA_VALU_PER_SLOT
-#define FMHA_VALU_PER_SLOT 8
+#define FMHA_VALU_PER_SLOT 7
 #endif
 constexpr int kValuPerSlot = FMHA_VALU_PER_SLOT;
 template <int I>

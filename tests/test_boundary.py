@@ -1,0 +1,182 @@
+"""The drop-in boundary without a GPU: the C-ABI library loads, exports every
+symbol include/*.h declares, the kernarg layout matches the reference's struct
+byte for byte (src/runner/params.hpp:18-64, offsets measured from the C
+header by a gcc-compiled probe), and the launcher's argument checks return the
+documented hipError_t codes.  No HIP call that needs a device is made.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+import pytest
+
+import fmha_native_amd as fmha
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+# the reference struct's field offsets (src/runner/params.hpp:18-64)
+REFERENCE_OFFSETS = {
+    "q": 0, "k": 8, "v": 16, "o": 24, "lse": 32, "seqlen_q": 40, "seqlen_k": 44, "nhead_q": 48, "nhead_k": 52,
+    "scale": 56, "stride_q": 60, "nhead_stride_q": 64, "batch_stride_q": 68, "stride_k": 72,
+    "nhead_stride_k": 76, "batch_stride_k": 80, "stride_v": 84, "nhead_stride_v": 88, "batch_stride_v": 92,
+    "stride_o": 96, "nhead_stride_o": 100, "batch_stride_o": 104, "seqstart_q": 112, "seqstart_k": 120,
+}
+KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_d64_bf16_msk0_varlen",
+                  "fmha_fwd_d64_bf16_msk1_varlen"]
+
+
+def header_c_functions():
+    """Names of the functions declared inside extern "C" blocks of include/*.h."""
+    names = []
+    for fn in sorted(os.listdir(INCLUDE)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"typedef struct.*?\}\s*\w+\s*;", "", text, flags=re.S)
+        for block in re.findall(r'extern "C" \{(.*?)\n\}', text, flags=re.S):
+            names += re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", block)
+    return names
+
+
+def exported_symbols(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = fmha.load_library()
+    names = header_c_functions()
+    assert {"fmha_fwd_d64_bf16", "fmha_fwd_d64_bf16_check", "fmha_fwd_d64_bf16_tile_config"} <= set(names)
+    syms = exported_symbols(fmha.LIB_PATH)
+    for n in names:
+        assert n in syms, n
+        assert getattr(lib, n) is not None
+
+
+def test_kernel_entries_exported():
+    """The four __global__ entries keep the reference's C++ names
+    (src/fused/kernel.cpp:55-99), so its callers link unchanged."""
+    syms = exported_symbols(fmha.LIB_PATH)
+    for e in KERNEL_ENTRIES:
+        mangled = f"_Z{len(e)}{e}13FmhaFwdParams"
+        assert mangled in syms, mangled
+
+
+def test_ctypes_layout_matches_reference():
+    assert ctypes.sizeof(fmha.FmhaFwdParams) == 128
+    assert ctypes.alignment(fmha.FmhaFwdParams) == 8
+    for name, off in REFERENCE_OFFSETS.items():
+        assert getattr(fmha.FmhaFwdParams, name).offset == off, name
+
+
+def test_c_header_layout_matches_reference():
+    """Compile include/fmha_fwd.h as plain C with gcc and print every offsetof."""
+    fields = list(REFERENCE_OFFSETS)
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"fmha_fwd.h\"\nint main(void){\n"
+    src += 'printf("%zu %zu\\n", sizeof(FmhaFwdParams), _Alignof(FmhaFwdParams));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof(FmhaFwdParams, {f}));\n'
+    src += "return 0;}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "probe.c")
+        exe = os.path.join(d, "probe")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-std=c11", f"-I{INCLUDE}", "-I/opt/rocm/include", c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    assert out[0] == "128" and out[1] == "8"
+    assert [int(x) for x in out[2:]] == [REFERENCE_OFFSETS[f] for f in fields]
+
+
+def test_tile_config():
+    assert fmha.tile_config() == {"kM0": 128, "kN0": 64, "kBlockSize": 256, "kHeadDim": 64}
+
+
+def test_missing_library_raises():
+    import importlib
+
+    mod = importlib.import_module("fmha_native_amd")
+    saved = mod._lib
+    try:
+        mod._lib = None
+        with pytest.raises(FileNotFoundError):
+            mod.load_library(os.path.join(ROOT, "does_not_exist.so"))
+    finally:
+        mod._lib = saved
+
+
+# ---------------------------------------------------------------- argument checks
+
+def valid_params(varlen=False, lse=True):
+    p = fmha.FmhaFwdParams()
+    base = 0x10000
+    p.q, p.k, p.v, p.o = base, base + 0x1000, base + 0x2000, base + 0x3000
+    p.lse = base + 0x4000 if lse else None
+    p.seqlen_q = p.seqlen_k = 128
+    p.nhead_q, p.nhead_k = 4, 2
+    p.scale = fmha.LOG2E / 8
+    for t in "qkvo":
+        setattr(p, f"stride_{t}", 64)
+        setattr(p, f"nhead_stride_{t}", 128 * 64)
+        setattr(p, f"batch_stride_{t}", 4 * 128 * 64)
+    if varlen:
+        p.seqstart_q = p.seqstart_k = base + 0x5000
+    return p
+
+
+INVALID = 1  # hipErrorInvalidValue
+
+
+@pytest.mark.parametrize("varlen", [False, True])
+def test_check_accepts_valid(varlen):
+    assert fmha.check_params(valid_params(varlen), 2, 0) == 0
+    assert fmha.check_params(valid_params(varlen), 2, 1) == 0
+    assert fmha.check_params(valid_params(varlen, lse=False), 0, 1) == 0
+
+
+def _mut(**kw):
+    p = valid_params(kw.pop("varlen", False))
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("params,batch,causal", [
+    (_mut(q=None), 1, 0),
+    (_mut(o=None), 1, 0),
+    (_mut(k=0x10002), 1, 0),                 # not 16-byte aligned
+    (_mut(lse=0x10002), 1, 0),               # LSE not 4-byte aligned
+    (_mut(stride_q=60), 1, 0),               # stride not a multiple of 8 (16-byte rows)
+    (_mut(stride_v=56), 1, 0),               # row shorter than 64 elements
+    (_mut(nhead_stride_k=-64), 1, 0),
+    (_mut(seqlen_q=-1), 1, 0),
+    (_mut(nhead_k=3), 1, 0),                 # nhead_q % nhead_k != 0
+    (_mut(nhead_k=0), 1, 0),
+    (_mut(seqstart_q=0x15000), 1, 0),        # only one seqstart pointer
+    (_mut(stride_k=1 << 23), 1, 0),          # offsets beyond 31 bits
+    (_mut(varlen=True, nhead_stride_q=128 * 64 + 8), 1, 0),  # varlen LSE head stride not in rows
+    (valid_params(), -1, 0),
+    (valid_params(), 1, 2),
+])
+def test_check_rejects(params, batch, causal):
+    assert fmha.check_params(params, batch, causal) == INVALID
+
+
+def test_null_params_pointer():
+    lib = fmha.load_library()
+    assert lib.fmha_fwd_d64_bf16_check(None, 1, 0) == INVALID
+
+
+# ---------------------------------------------------------------- bench contract
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)

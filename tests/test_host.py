@@ -1,0 +1,109 @@
+"""Host-side logic without a GPU: input generators, problem geometry, FLOP
+conventions and the configuration tables."""
+import numpy as np
+import pytest
+
+import fmha_native_amd as fmha
+import oracle
+from configs import K_ALL_FULL, all_full, baseline_problems
+from fmha_native_amd.problem import Problem, bhsd_to_bshd, bshd_to_bhsd
+
+
+@pytest.mark.parametrize("seed,n", [(42, 4096), (7, 1000), (123456, 33)])
+def test_fill_ref_two_implementations_agree(seed, n):
+    """The product's generator (C++, runner.cpp) and the oracle's (C) restate
+    the reference's fill_random (src/runner/buffers.cpp:99-127) separately."""
+    a = fmha.fill_ref(seed, n, n + 5, n + 7)
+    b = oracle.fill_ref(seed, n, n + 5, n + 7)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_fill_ref_value_set():
+    """bf16((r % 1000 - 500) / 5000): |x| <= 0.1 and 1000 distinct fp32 sources."""
+    q, _, _ = fmha.fill_ref(42, 200000, 0, 0)
+    f = (q.astype(np.uint32) << 16).view(np.float32)
+    assert np.abs(f).max() <= 0.1
+    assert f.min() == np.float32(-0.1) or f.min() < -0.099
+    src = np.arange(-500, 500, dtype=np.float32) / np.float32(5000.0)
+    allowed = np.unique((src.view(np.uint32) >> 16).astype(np.uint16))
+    assert np.isin(q, allowed).all()
+
+
+def test_fill_normal_properties():
+    a = fmha.fill_normal(42, 1 << 20)
+    b = fmha.fill_normal(42, 1 << 20)
+    c = fmha.fill_normal(43, 1 << 20)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    f = (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    assert abs(f.mean()) < 5e-3 and abs(f.std() - 1.0) < 5e-3
+    # prefix-stable (counter-based): the first n values do not depend on the length
+    assert np.array_equal(fmha.fill_normal(42, 1000), a[:1000])
+    # scaling by 2 is exact in bf16
+    d = fmha.fill_normal(42, 1 << 16, 2.0)
+    fd = (d.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(fd, 2 * f[: 1 << 16].astype(np.float32))
+
+
+def test_varlen_lengths():
+    a = fmha.varlen_lengths(42, 8, 128, 4096)
+    assert a == fmha.varlen_lengths(42, 8, 128, 4096)
+    assert a != fmha.varlen_lengths(43, 8, 128, 4096)
+    assert all(128 <= s <= 4096 for s in a)
+    assert sum(s % 64 != 0 for s in a) >= 4
+    with pytest.raises(ValueError):
+        fmha.varlen_lengths(1, 4, 10, 5)
+
+
+def test_problem_geometry():
+    p = Problem(batch=2, nhead_q=8, nhead_k=2, seqlen_q=100, seqlen_k=300, causal=True, lse=True)
+    assert p.sizes() == (2 * 8 * 100 * 64, 2 * 2 * 300 * 64, 2 * 8 * 100)
+    assert p.strides()["q"] == (64, 100 * 64, 8 * 100 * 64)
+    assert p.strides()["k"] == (64, 300 * 64, 2 * 300 * 64)
+    b = Problem(batch=2, nhead_q=8, nhead_k=2, seqlen_q=100, seqlen_k=300, layout="bshd")
+    assert b.strides()["q"] == (8 * 64, 64, 100 * 8 * 64)
+    v = Problem(batch=0, nhead_q=4, seqlen_q=0, varlen_seqs=(5, 70, 33))
+    assert v.batch == 3 and v.seqlen_q == 70 and v.seqlen_k == 70
+    assert v.seqstart().tolist() == [0, 5, 75, 108]
+    assert v.strides()["q"] == (64, 108 * 64, 0)
+    with pytest.raises(ValueError):
+        Problem(batch=1, nhead_q=6, nhead_k=4, seqlen_q=8)
+
+
+def test_layout_roundtrip():
+    a = np.arange(2 * 3 * 5 * 64, dtype=np.uint16)
+    assert np.array_equal(bshd_to_bhsd(bhsd_to_bshd(a, 2, 3, 5), 2, 3, 5), a)
+    t = bhsd_to_bshd(a, 2, 3, 5).reshape(2, 5, 3, 64)
+    assert np.array_equal(t[1, 4, 2], a.reshape(2, 3, 5, 64)[1, 2, 4])
+
+
+def test_flop_conventions():
+    """src/bench_fmha_fwd.cpp:225-226: 4*B*H*Sq*Sk*D, x0.5 causal."""
+    cfg = {k: v[0] for k, v in baseline_problems().items()}
+    assert cfg["cfg1"].flops() == 8388608
+    assert cfg["cfg2"].flops() == 68719476736
+    assert cfg["cfg3"].flops() == 137438953472  # 4*16*8192^2*64 * 0.5
+    assert cfg["cfg5"].flops() == 409600000000  # 4*2*40000^2*64 * 0.5
+    # exact causal count: sum over rows of the visible keys
+    p = Problem(batch=1, nhead_q=1, seqlen_q=4, seqlen_k=6, causal=True)
+    assert p.exact_flops() == 4 * 64 * (3 + 4 + 5 + 6)
+    assert Problem(batch=1, nhead_q=2, seqlen_q=8).exact_flops() == Problem(batch=1, nhead_q=2, seqlen_q=8).flops()
+
+
+def test_io_bytes():
+    cfg = {k: v[0] for k, v in baseline_problems().items()}
+    assert cfg["cfg1"].io_bytes() == 132096
+    assert cfg["cfg2"].io_bytes() == 67108864
+    assert cfg["cfg3"].io_bytes() == 67633152
+    assert cfg["cfg5"].io_bytes() == 41280000
+
+
+def test_config_tables():
+    assert len(K_ALL_FULL) == 63
+    names = [r[0] for r in K_ALL_FULL]
+    assert len(set(names)) == len(names)
+    probs = all_full()
+    assert all(p.nhead_q % p.nhead_k == 0 for p in probs)
+    cfg4 = baseline_problems()["cfg4"][0]
+    assert cfg4.batch == 8 and cfg4.causal and cfg4.lse
+    assert baseline_problems()["cfg5"][1] == 2.0
