@@ -10,9 +10,11 @@ configuration is reported under ``also``.  A step is one launch of the
 forward over the whole batch with Q/K/V already resident in HBM.  Inputs are
 synthetic N(0,1) bf16 (seed 42).
 
-The CPU baseline is the reference-faithful CPU oracle (oracle/, the
-restatement of src/runner/cpu_ref.cpp) timed on this host on a bounded
-row sample of the same workload.  Only this leg touches oracle/.
+The CPU baseline is the reference's own CPU path, cpu_ref_verify, compiled
+from its sources into oracle/_ref/ref_verify and timed over the whole dense
+workload on this host ("kind": "reference"); where that harness was not built,
+the faithful C restatement (oracle/) on a bounded row sample ("kind": "port").
+Only this leg touches oracle/.
 """
 import argparse
 import json
@@ -89,6 +91,36 @@ def time_problem(prob, steps, warmup, torch):
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
     return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "host": host}
+
+
+REF_VERIFY = os.path.join(ROOT, "oracle", "_ref", "ref_verify")
+
+
+def cpu_baseline_reference(prob):
+    """The reference's own CPU path, cpu_ref_verify (src/runner/cpu_ref.cpp:14-311,
+    compiled from its sources into oracle/_ref/ref_verify), over the whole
+    workload, timed by the harness around that one call.  None if not built."""
+    import subprocess
+
+    if not os.path.exists(REF_VERIFY) or prob.causal or prob.lse:
+        return None
+    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(prob.nhead_q), "-s", str(prob.seqlen_q), "--seed", "42"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return None
+    res = [json.loads(l.split(" ", 1)[1]) for l in r.stdout.splitlines() if l.startswith("REF_VERIFY ")]
+    if not res:
+        return None
+    t, thr = res[0]["cpu_ref_seconds"], res[0]["threads"]
+    return {
+        "value": prob.flops() / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": thr,
+        "kind": "reference",
+        "sample": f"the reference's cpu_ref_verify over the full B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q} "
+                  f"workload (its fill_random(42) inputs; time does not depend on values), {t:.2f} s on {thr} "
+                  f"OpenMP threads; its check of this kernel's O: pass={res[0]['pass']}",
+    }
 
 
 def cpu_baseline(prob, host, budget_s=10.0):
@@ -172,7 +204,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg2, r2["host"])
+        cpu = cpu_baseline_reference(cfg2) or cpu_baseline(cfg2, r2["host"])
 
     achieved = r2["tflops"]
     line = {

@@ -107,3 +107,28 @@ def test_config_tables():
     cfg4 = baseline_problems()["cfg4"][0]
     assert cfg4.batch == 8 and cfg4.causal and cfg4.lse
     assert baseline_problems()["cfg5"][1] == 2.0
+
+
+def test_sweep_protocol_and_table(tmp_path, capsys):
+    """fmha_native_amd.sweep: 6 runs per config, first dropped, the reference's
+    table format (scripts/run-benchmark.sh:56-99)."""
+    from fmha_native_amd import sweep
+
+    counter = tmp_path / "n"
+    fake = tmp_path / "bench"
+    # run k of each config reports Avg = k ms (the dropped first run is 1 ms)
+    fake.write_text("#!/bin/bash\nn=$(cat %s 2>/dev/null || echo 0); n=$((n %% 6 + 1)); echo $n > %s\n"
+                    "echo \"Avg: $n.000 ms\"; echo \"min=0.$n ms\"; echo \"TFLOPS: ${n}0.00\"\n" % (counter, counter))
+    fake.chmod(0o755)
+    assert sweep.main(["--bench", str(fake), "--mask", "1"]) == 0
+    out = capsys.readouterr().out.splitlines()
+    assert out[0] == "Benchmark: 8 configs (WARMUP=5 ITERS=20 RUNS=6 DROP=1 MASK=1)"
+    rows = [l for l in out if "|" in l][1:]
+    assert len(rows) == 8
+    assert rows[1] == "   4  16   2048   64 |      4.000      0.200      40.00"
+    bad = tmp_path / "bad"
+    bad.write_text("#!/bin/bash\necho 'HIP error 98 (invalid device function)'; exit 1\n")
+    bad.chmod(0o755)
+    sweep.main(["--bench", str(bad)])
+    out = capsys.readouterr().out
+    assert "ERROR" in out and "HIP error 98" in out
