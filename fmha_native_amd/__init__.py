@@ -25,7 +25,7 @@ import numpy as np
 __all__ = [
     "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
     "tile_config", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
-    "LOG2E", "HIP_ERROR_INVALID_VALUE",
+    "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANTS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -77,6 +77,8 @@ def load_library(path=LIB_PATH):
     P = ctypes.POINTER(FmhaFwdParams)
     lib.fmha_fwd_d64_bf16.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.fmha_fwd_d64_bf16.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_variant.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.fmha_fwd_d64_bf16_variant.restype = ctypes.c_int
     lib.fmha_fwd_d64_bf16_check.argtypes = [P, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_check.restype = ctypes.c_int
     ip = ctypes.POINTER(ctypes.c_int)
@@ -94,9 +96,20 @@ def load_library(path=LIB_PATH):
     return lib
 
 
-def fmha_fwd_d64_bf16(params, batch, causal, stream=None):
-    """Launch on ``stream`` (a hipStream_t as int, or None for the null stream)."""
-    rc = load_library().fmha_fwd_d64_bf16(ctypes.byref(params), int(batch), int(causal), stream)
+VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV = 0, 1, 2
+VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV}
+
+
+def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
+    """Launch on ``stream`` (a hipStream_t as int, or None for the null stream).
+
+    ``variant``: VARIANT_AUTO (the launcher's choice), VARIANT_REGULAR (the
+    reference-named entries) or VARIANT_SPLITKV (the split-KV entries)."""
+    lib = load_library()
+    if variant == VARIANT_AUTO:
+        rc = lib.fmha_fwd_d64_bf16(ctypes.byref(params), int(batch), int(causal), stream)
+    else:
+        rc = lib.fmha_fwd_d64_bf16_variant(ctypes.byref(params), int(batch), int(causal), int(variant), stream)
     if rc != HIP_SUCCESS:
         raise FmhaError(rc)
 

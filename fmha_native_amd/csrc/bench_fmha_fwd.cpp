@@ -10,6 +10,7 @@
 //   --dist ref|normal   reference +-0.1 generator (default) or N(0,1)
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
+//   --variant auto|regular|splitkv   kernel form (default: the launcher's choice)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
 
@@ -41,6 +42,7 @@ struct Config {
     int mask = 0, lse = 0, warmup = 5, iters = 20;
     unsigned seed = 42;
     std::string dist = "ref";
+    int variant = FMHA_VARIANT_AUTO;
     float scale_inputs = 1.0f;
     std::vector<int> varlen_seqs;
 };
@@ -60,7 +62,8 @@ static void usage(const char* prog) {
            "  --iters N        Benchmark iterations [20]\n"
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
-           "  --scale-inputs X Multiplier for normal inputs [1]\n",
+           "  --scale-inputs X Multiplier for normal inputs [1]\n"
+           "  --variant V      auto|regular|splitkv kernel form [auto]\n",
            prog);
 }
 
@@ -80,6 +83,7 @@ static Config parse(int argc, char** argv) {
                                    {"seed", required_argument, 0, 3},
                                    {"dist", required_argument, 0, 4},
                                    {"scale-inputs", required_argument, 0, 5},
+                                   {"variant", required_argument, 0, 7},
                                    {"help", no_argument, 0, 0},
                                    {0, 0, 0, 0}};
     int ch, idx;
@@ -107,6 +111,12 @@ static Config parse(int argc, char** argv) {
             case 3: c.seed = (unsigned)strtoul(optarg, nullptr, 10); break;
             case 4: c.dist = optarg; break;
             case 5: c.scale_inputs = (float)atof(optarg); break;
+            case 7:
+                if (!strcmp(optarg, "auto")) c.variant = FMHA_VARIANT_AUTO;
+                else if (!strcmp(optarg, "regular")) c.variant = FMHA_VARIANT_REGULAR;
+                else if (!strcmp(optarg, "splitkv")) c.variant = FMHA_VARIANT_SPLITKV;
+                else { fprintf(stderr, "Error: --variant must be auto, regular or splitkv\n"); exit(1); }
+                break;
             case 0: usage(argv[0]); exit(0);
             default: usage(argv[0]); exit(1);
         }
@@ -195,7 +205,7 @@ int main(int argc, char** argv) {
     }
 
     auto launch = [&]() {
-        hipError_t e = fmha_fwd_d64_bf16(&p, c.batch, c.mask, nullptr);
+        hipError_t e = fmha_fwd_d64_bf16_variant(&p, c.batch, c.mask, c.variant, nullptr);
         if (e != hipSuccess) {
             fprintf(stderr, "fmha_fwd_d64_bf16 failed: %d (%s)\n", (int)e, hipGetErrorString(e));
             exit(1);

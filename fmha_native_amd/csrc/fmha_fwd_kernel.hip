@@ -61,7 +61,6 @@ constexpr int kTileN = FMHA_KN0;               // 64 keys per tile
 constexpr int kRowBytes = 128;                 // 64 bf16 per K/V row in LDS
 constexpr int kTileBytes = kTileN * kRowBytes; // 8 KiB
 constexpr int kRing = 4;                       // stages per ring (K and V)
-constexpr int kLdsBytes = 2 * kRing * kTileBytes;  // 64 KiB in 2*kRing separate arrays
 constexpr int kLoadsPerTile = 2;                   // 1 KiB DMA per load, per wave
 constexpr float kGrowSum = 256.0f;                 // tile-sum bound of the speculative softmax
 constexpr float kMaxSeed = -5000.0f;               // raw-score running max seed (pipeline.hpp:248-252)
@@ -134,27 +133,32 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Schedule of one pipelined iteration: 16 slots of {1 MFMA, DS reads for the
-// MFMA two slots ahead, kValuPerSlot VALU}; GEMM1 MFMAs take two tr_b16
-// reads, GEMM0 MFMAs one b128 read.  Groups are filled in order, respecting
-// dependences.  The softmax of a tile is ~117 VALU (32 fma, 32 exp, 35 add,
-// 16 cvt_pk, bookkeeping), spread evenly over the 16 MFMAs.
+// Schedule of one pipelined iteration: 16 slots of {1 MFMA, the DS reads of
+// the MFMA kDsAhead slots later, kValuPerSlot VALU}.  MFMAs 0-7 are GEMM1's
+// (two tr_b16 reads each), 8-15 GEMM0's (one b128 read each); the reads of
+// MFMAs 0 .. kDsAhead-1 open the iteration.  Groups are filled in order,
+// respecting dependences.  The softmax of a tile is ~117 VALU (32 fma, 32
+// exp, 35 add, 16 cvt_pk, bookkeeping), spread evenly over the 16 MFMAs.
 #ifndef FMHA_VALU_PER_SLOT
 #define FMHA_VALU_PER_SLOT 7
 #endif
+#ifndef FMHA_DS_AHEAD
+#define FMHA_DS_AHEAD 2
+#endif
 constexpr int kValuPerSlot = FMHA_VALU_PER_SLOT;
+constexpr int kDsAhead = FMHA_DS_AHEAD;
+constexpr int ds_reads_of_mfma(int m) { return m < 8 ? 2 : (m < 16 ? 1 : 0); }
+constexpr int ds_reads_before(int n) { return n <= 0 ? 0 : ds_reads_of_mfma(n - 1) + ds_reads_before(n - 1); }
 template <int I>
 __device__ __forceinline__ void sched_slot() {
     __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-    if constexpr (I < 6)
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-    else if constexpr (I < 14)
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 1, 0);
+    if constexpr (ds_reads_of_mfma(I + kDsAhead) > 0)
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, ds_reads_of_mfma(I + kDsAhead), 0);
     __builtin_amdgcn_sched_group_barrier(kSchedVALU, kValuPerSlot, 0);
 }
 template <int... Is>
 __device__ __forceinline__ void sched_iteration(std::integer_sequence<int, Is...>) {
-    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, ds_reads_before(kDsAhead), 0);
     (sched_slot<Is>(), ...);
 }
 
@@ -166,11 +170,19 @@ struct Softmax {
     float l_tile;  // this lane's sum of P over the current tile
 };
 
-// One block = one kTileM-row M-tile of (batch b, head h).
-template <bool kCausal, bool kVarlen>
+// One block = one kTileM-row M-tile of (batch b, head h), computed by kSplit
+// groups of kWaves waves.  Group g walks the g-th contiguous share of the
+// M-tile's key tiles with its own half of every LDS stage; with kSplit = 2
+// the groups' partial (O^T, m, l) are merged through LDS at the end (group 1
+// hands over, group 0 writes O and LSE).  All groups run the same number of
+// iterations, so the block-wide barriers stay in step.
+template <bool kCausal, bool kVarlen, int kSplit>
 __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, const Ring& ring) {
+    static_assert(kSplit == 1 || kSplit == 2, "one or two key-range groups per block");
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int group = kSplit == 1 ? 0 : wave_id / kWaves;                  // key-range group
+    const int wave = kSplit == 1 ? wave_id : wave_id % kWaves;             // wave within the group
     const int l32 = lane & 31;
     const int hi = lane >> 5;
 
@@ -225,6 +237,11 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         kv_end = e < 0 ? 0 : (e > sk ? sk : e);
     }
     const int ntiles = (kv_end + kTileN - 1) / kTileN;
+    // this group's key tiles: global tiles [tile0, tile0 + ntg) (the loops
+    // below count group-local tiles 0 .. ntg-1); tiles >= tile_end are dead
+    const int ntg = (ntiles + kSplit - 1) / kSplit;
+    const int tile0 = group * ntg;
+    const int tile_end = min(ntiles, tile0 + ntg);
 
     const int wrow0 = row0 + wave * kRowsPerWave;  // first query row of this wave
     const int my_row = wrow0 + l32;                // this lane's query row
@@ -257,23 +274,26 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int v_ld_off1 = (ld_row + 8) * p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row + 8)) << 4);
     const int k_tile_step = kTileN * p.stride_k * 2;
     const int v_tile_step = kTileN * p.stride_v * 2;
-    const int wave_off = (2 * wave) * 1024;
+    const int goff = group * kTileBytes;  // this group's half of every LDS stage
+    const int wave_off = goff + (2 * wave) * 1024;
 
-    // Tile t's K lands in K stage t % kRing, its V in V stage t % kRing.  The
-    // tile's own descriptor (base at the tile's first row, num_records = bytes
-    // left; 0 for a dead tile) is built in scalar registers, so the per-lane
-    // offsets stay loop-invariant.
+    // Local tile t's K lands in K stage t % kRing, its V in V stage t % kRing.
+    // The tile's own descriptor (base at the tile's first row, num_records =
+    // bytes left; 0 for a dead tile) is built in scalar registers, so the
+    // per-lane offsets stay loop-invariant.
     auto issue_k = [&](int tile, auto stage_c) {
         lds_char* dst = ring.k[decltype(stage_c)::value] + wave_off;
-        const uint32_t t0 = (uint32_t)tile * (uint32_t)k_tile_step;
-        const auto r = make_rsrc((const char*)kbase + t0, tile < ntiles ? kbytes - t0 : 0u);
+        const int gt = tile0 + tile;
+        const uint32_t t0 = (uint32_t)gt * (uint32_t)k_tile_step;
+        const auto r = make_rsrc((const char*)kbase + t0, gt < tile_end ? kbytes - t0 : 0u);
         lds_dma_16(r, dst, k_ld_off0);
         lds_dma_16(r, dst + 1024, k_ld_off1);
     };
     auto issue_v = [&](int tile, auto stage_c) {
         lds_char* dst = ring.v[decltype(stage_c)::value] + wave_off;
-        const uint32_t t0 = (uint32_t)tile * (uint32_t)v_tile_step;
-        const auto r = make_rsrc((const char*)vbase + t0, tile < ntiles ? vbytes - t0 : 0u);
+        const int gt = tile0 + tile;
+        const uint32_t t0 = (uint32_t)gt * (uint32_t)v_tile_step;
+        const auto r = make_rsrc((const char*)vbase + t0, gt < tile_end ? vbytes - t0 : 0u);
         lds_dma_16(r, dst, v_ld_off0);
         lds_dma_16(r, dst + 1024, v_ld_off1);
     };
@@ -284,7 +304,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     {
         const int f = k_swz(l32);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) k_rd[t] = l32 * kRowBytes + (((2 * t + hi) ^ f) << 4);
+        for (int t = 0; t < 4; ++t) k_rd[t] = goff + l32 * kRowBytes + (((2 * t + hi) ^ f) << 4);
     }
     // V^T (A of GEMM1) via ds_read_b64_tr_b16: in each 16-lane group, source
     // lane 4e + c supplies the address of 4 d-values (d = dbase + 4c) of key
@@ -298,13 +318,13 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
             const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-            v_rd[db] = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
+            v_rd[db] = goff + row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
         }
     }
 
     const float scale = p.scale;  // log2(e)/sqrt(D)
     Softmax sm{kMaxSeed, 0.0f, 0.0f};
-    constexpr int kBlockSize = FMHA_KBLOCK;
+    constexpr int kGroupSize = kWaves * 64;  // threads per key-range group
     f32x16 oacc[2];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
@@ -314,7 +334,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     // ---- the three pipeline stages (stage indices are compile-time) ----
     // GEMM0 of the tile in K stage KS: S^T[kb] = K[kb] . Q^T
     auto gemm0 = [&](auto ks_c, f32x16* s) {
-        const lds_char* st = ring.k[decltype(ks_c)::value];
+        const lds_char* st = ring.k[decltype(ks_c)::value];  // k_rd includes goff
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             f32x16 acc = {};
@@ -325,7 +345,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     };
     // GEMM1 of the tile in V stage VS: O^T[db] += V^T[db] . P^T
     auto gemm1 = [&](auto vs_c, const bf16x8* pp) {
-        const lds_char* st = ring.v[decltype(vs_c)::value];
+        const lds_char* st = ring.v[decltype(vs_c)::value];  // v_rd includes goff
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -335,9 +355,9 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
                     oacc[db] = mfma(lds_read_vt(st + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[2 * kb + k],
                                     oacc[db]);
     };
-    // mask of tile t: keys >= sk, and (causal) keys > row + shift
+    // mask of local tile t: keys >= sk, and (causal) keys > row + shift
     auto mask_tile = [&](int t, f32x16* s) {
-        const int key0 = t * kTileN;
+        const int key0 = (tile0 + t) * kTileN;
         const bool need = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
         if (need) {
             // element (kb, r) holds key key0 + 4h + c with c = 32kb + 8(r/4) + r%4;
@@ -457,16 +477,18 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     using P2 = std::integral_constant<int, 2>;
     using P3 = std::integral_constant<int, 3>;
 
-    if (ntiles > 0) {
+    if (ntg > 0) {
         // GEMM1(-1) of iteration 0 runs on P = 0 and a zeroed V stage, which
         // contributes exactly 0 and keeps the loop body branch-free.
 #pragma unroll
         for (int i = 0; i < 4; ++i) pbuf[1][i] = bf16x8{};
         {
             typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
-            lds_i32x4* z = (lds_i32x4*)ring.v[kRing - 1];
-            z[threadIdx.x] = i32x4{};
-            z[threadIdx.x + kBlockSize] = i32x4{};
+            static_assert(kTileBytes == 2 * kGroupSize * 16, "two 16-byte stores per thread zero a stage");
+            lds_i32x4* z = (lds_i32x4*)(ring.v[kRing - 1] + goff);
+            const int tig = threadIdx.x % kGroupSize;
+            z[tig] = i32x4{};
+            z[tig + kGroupSize] = i32x4{};
         }
         // prologue: K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once K0 landed
         issue_k(0, P0{});
@@ -484,13 +506,13 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         mask_tile(0, sacc[0]);
         sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]));
         int t = 0;
-        for (; t + kRing <= ntiles; t += kRing) {
+        for (; t + kRing <= ntg; t += kRing) {
             iteration(t, P0{});
             iteration(t + 1, P1{});
             iteration(t + 2, P2{});
             iteration(t + 3, P3{});
         }
-        const int rem = ntiles - t;
+        const int rem = ntg - t;
         if (rem == 0) {
             last_gemm1(P3{});
         } else {
@@ -507,6 +529,40 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
                 }
             }
         }
+    }
+
+    if constexpr (kSplit == 2) {
+        // Hand-over: group 1 leaves its partial (O^T, m_ref, l_part) in LDS and
+        // exits; group 0 folds it into its own.  The K stages are free: their
+        // last reads (GEMM0 of the final iteration) completed before the
+        // barrier in last_gemm1.  Wave w of either group owns the same 32 rows
+        // and lane L the same (row, columns), so lane L meets lane L.
+        typedef __attribute__((address_space(3))) float lds_float;
+        // element e of lane L at x[64e + L], wave w in K stage w (a select
+        // chain: a runtime-indexed table of LDS addresses cannot be emitted)
+        lds_char* xs = wave == 0 ? ring.k[0] : wave == 1 ? ring.k[1] : wave == 2 ? ring.k[2] : ring.k[3];
+        lds_float* x = (lds_float*)xs;
+        static_assert(34 * 64 * 4 <= kSplit * kTileBytes, "hand-over fits one K stage");
+        if (group == 1) {
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) x[(16 * db + r) * 64 + lane] = oacc[db][r];
+            x[32 * 64 + lane] = sm.m_ref;
+            x[33 * 64 + lane] = sm.l_part;
+        }
+        __syncthreads();
+        if (group == 1) return;
+        const float m1 = x[32 * 64 + lane];
+        const float m = fmaxf(sm.m_ref, m1);
+        const float a0 = __builtin_amdgcn_exp2f((sm.m_ref - m) * scale);
+        const float a1 = __builtin_amdgcn_exp2f((m1 - m) * scale);
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] = a0 * oacc[db][r] + a1 * x[(16 * db + r) * 64 + lane];
+        sm.l_part = a0 * sm.l_part + a1 * x[33 * 64 + lane];
+        sm.m_ref = m;
     }
 
     // ---- epilogue: O = O^T / l (rows < sq; the buffer bound drops the rest),
@@ -547,30 +603,55 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 using namespace fmha_gfx950;
 
 // ---- the four entries (reference src/fused/kernel.cpp:55-99).  Grid
-// (nhead_q, ceil(seqlen_q/kM0), batch).  Causal entries run the heaviest
-// M-tiles first (kernel.cpp:73,96). ----
+// (nhead_q, ceil(seqlen_q/kM0), batch), kBlockSize threads.  Causal entries
+// run the heaviest M-tiles first (kernel.cpp:73,96). ----
 #define FMHA_ENTRY_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(2, 2)))
-// eight distinct LDS arrays = the K and V ring stages
-#define FMHA_RING(r)                                                                                          \
-    __shared__ __attribute__((aligned(1024))) char r##_k0[kTileBytes], r##_k1[kTileBytes], r##_k2[kTileBytes], \
-        r##_k3[kTileBytes], r##_v0[kTileBytes], r##_v1[kTileBytes], r##_v2[kTileBytes], r##_v3[kTileBytes];   \
-    const Ring r{{(lds_char*)r##_k0, (lds_char*)r##_k1, (lds_char*)r##_k2, (lds_char*)r##_k3},                \
+// eight distinct LDS arrays = the K and V ring stages (each `bytes` long)
+#define FMHA_RING(r, bytes)                                                                                     \
+    __shared__ __attribute__((aligned(1024))) char r##_k0[bytes], r##_k1[bytes], r##_k2[bytes], r##_k3[bytes],   \
+        r##_v0[bytes], r##_v1[bytes], r##_v2[bytes], r##_v3[bytes];                                             \
+    const Ring r{{(lds_char*)r##_k0, (lds_char*)r##_k1, (lds_char*)r##_k2, (lds_char*)r##_k3},                  \
                  {(lds_char*)r##_v0, (lds_char*)r##_v1, (lds_char*)r##_v2, (lds_char*)r##_v3}};
 static_assert(kRing == 4, "FMHA_RING declares four stages per ring");
 
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0(FmhaFwdParams params) {
-    FMHA_RING(ring)
-    fwd_mtile<false, false>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<false, false, 1>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1(FmhaFwdParams params) {
-    FMHA_RING(ring)
-    fwd_mtile<true, false>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, false, 1>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0_varlen(FmhaFwdParams params) {
-    FMHA_RING(ring)
-    fwd_mtile<false, true>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<false, true, 1>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen(FmhaFwdParams params) {
-    FMHA_RING(ring)
-    fwd_mtile<true, true>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, true, 1>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+}
+
+// ---- split-KV entries (this build's own; no counterpart in the reference):
+// same grid, 2*kBlockSize threads, two key-range groups per M-tile merged in
+// LDS.  For grids with too few blocks to fill the GPU, or causal grids whose
+// heaviest M-tile outlasts the average load per CU. ----
+#define FMHA_SPLIT_ATTRS \
+    __global__ __launch_bounds__(FMHA_SPLIT_KBLOCK) __attribute__((amdgpu_waves_per_eu(2, 2)))
+static_assert(FMHA_SPLIT_KBLOCK == 2 * FMHA_KBLOCK, "two groups of kBlockSize threads");
+
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk0(FmhaFwdParams params) {
+    FMHA_RING(ring, 2 * kTileBytes)
+    fwd_mtile<false, false, 2>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1(FmhaFwdParams params) {
+    FMHA_RING(ring, 2 * kTileBytes)
+    fwd_mtile<true, false, 2>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk0_varlen(FmhaFwdParams params) {
+    FMHA_RING(ring, 2 * kTileBytes)
+    fwd_mtile<false, true, 2>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1_varlen(FmhaFwdParams params) {
+    FMHA_RING(ring, 2 * kTileBytes)
+    fwd_mtile<true, true, 2>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }

@@ -90,6 +90,11 @@ typedef struct FmhaFwdParams {
 #define FMHA_KN0 64
 #define FMHA_KBLOCK 256
 #define FMHA_HEAD_DIM 64
+/* Threads per block of the split-KV entries (two groups of FMHA_KBLOCK, each
+ * walking half of an M-tile's key range; this build's own, launched by
+ * fmha_fwd_d64_bf16() when the grid is too small or too unbalanced to fill
+ * the GPU). */
+#define FMHA_SPLIT_KBLOCK 512
 
 /* Launch the D64 BF16 forward pass on `stream`.
  *   params : kernarg (host memory; copied by value)
@@ -97,10 +102,26 @@ typedef struct FmhaFwdParams {
  *   causal : 0 = no mask (reference --mask 0), 1 = bottom-right causal (--mask 1)
  * Returns hipSuccess, hipErrorInvalidValue for rejected arguments (nothing is
  * launched), or the launch error.  Asynchronous like any kernel launch; it
- * allocates nothing and keeps no state, so concurrent calls are safe.
+ * allocates nothing (its only state is a per-device cache of the compute-unit
+ * count), so concurrent calls are safe.  Grids with at most 2 blocks per
+ * compute unit run the split-KV form (see fmha_fwd_d64_bf16_variant).
  * Replaces src/bench_fmha_fwd.cpp:174-191. */
 hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
                              hipStream_t stream);
+
+/* The same launch with the kernel form chosen by the caller (this build's
+ * own; no counterpart in the reference):
+ *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: split-KV when the
+ *                         grid has at most 2 blocks per compute unit
+ *   FMHA_VARIANT_REGULAR  the four reference-named entries (kBlockSize threads)
+ *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
+ * Both forms give the same results up to fp32 rounding order.  An unknown
+ * variant returns hipErrorInvalidValue. */
+#define FMHA_VARIANT_AUTO 0
+#define FMHA_VARIANT_REGULAR 1
+#define FMHA_VARIANT_SPLITKV 2
+hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
+                                     hipStream_t stream);
 
 /* Argument checks of fmha_fwd_d64_bf16 without launching (host only, no GPU
  * needed).  Returns hipSuccess or hipErrorInvalidValue. */
@@ -140,6 +161,12 @@ __global__ void fmha_fwd_d64_bf16_msk0(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_msk1_varlen(FmhaFwdParams params);
+/* Split-KV forms of the same four (no counterpart in the reference): same
+ * grid, block FMHA_SPLIT_KBLOCK, same results up to fp32 rounding order. */
+__global__ void fmha_fwd_d64_bf16_splitkv_msk0(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_splitkv_msk1(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_splitkv_msk0_varlen(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_splitkv_msk1_varlen(FmhaFwdParams params);
 #endif
 #endif /* __cplusplus */
 

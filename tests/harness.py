@@ -58,7 +58,7 @@ def build_params(prob, dq, dk, dv, do, dlse, dseq):
     return p
 
 
-def run_kernel(prob, q, k, v, stream=None):
+def run_kernel(prob, q, k, v, stream=None, variant=0):
     """One launch through the C-ABI; returns (O bits uint16, LSE float32 or None)."""
     import torch
 
@@ -71,17 +71,17 @@ def run_kernel(prob, q, k, v, stream=None):
     p = build_params(prob, dq, dk, dv, do, dlse, dseq)
     if stream is None:
         stream = torch.cuda.current_stream().cuda_stream
-    fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), stream)
+    fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), stream, variant)
     torch.cuda.synchronize()
     o = do.cpu().numpy().view(np.uint16)
     lse = dlse.cpu().numpy() if dlse is not None else None
     return o, lse
 
 
-def check_problem(prob, dist="ref", seed=42, mult=1.0, rule="reference"):
+def check_problem(prob, dist="ref", seed=42, mult=1.0, rule="reference", variant=0):
     """Kernel vs oracle on seeded inputs.  Returns a dict of results."""
     q, k, v = make_inputs(prob, dist, seed, mult)
-    o_bits, lse = run_kernel(prob, q, k, v)
+    o_bits, lse = run_kernel(prob, q, k, v, variant=variant)
     o_ref, lse_ref = oracle.run(prob, q, k, v)
     o_k = verify.bf16_bits_to_f32(o_bits)
     res = {"name": prob.name}
@@ -96,7 +96,7 @@ def check_problem(prob, dist="ref", seed=42, mult=1.0, rule="reference"):
     return res
 
 
-def check_baseline(prob, mult=1.0, seed=42):
+def check_baseline(prob, mult=1.0, seed=42, variant=0):
     """Benchmark-configuration check (N(0,1)*mult inputs).
 
     O must be within 1e-2 + 1e-2|O| of (a) the oracle without the reference's
@@ -106,7 +106,7 @@ def check_baseline(prob, mult=1.0, seed=42):
     reported as ``o_plain``.  LSE within 1e-3 of the oracle.
     """
     q, k, v = make_inputs(prob, "normal", seed, mult)
-    o_bits, lse = run_kernel(prob, q, k, v)
+    o_bits, lse = run_kernel(prob, q, k, v, variant=variant)
     o_t, lse_t = oracle.run(prob, q, k, v)
     o_u, _ = oracle.run(prob, q, k, v, p_trunc=False)
     o_k = verify.bf16_bits_to_f32(o_bits)

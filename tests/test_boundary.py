@@ -28,6 +28,8 @@ REFERENCE_OFFSETS = {
 }
 KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_d64_bf16_msk0_varlen",
                   "fmha_fwd_d64_bf16_msk1_varlen"]
+SPLIT_ENTRIES = ["fmha_fwd_d64_bf16_splitkv_msk0", "fmha_fwd_d64_bf16_splitkv_msk1",
+                 "fmha_fwd_d64_bf16_splitkv_msk0_varlen", "fmha_fwd_d64_bf16_splitkv_msk1_varlen"]
 
 
 def header_c_functions():
@@ -64,7 +66,7 @@ def test_kernel_entries_exported():
     """The four __global__ entries keep the reference's C++ names
     (src/fused/kernel.cpp:55-99), so its callers link unchanged."""
     syms = exported_symbols(fmha.LIB_PATH)
-    for e in KERNEL_ENTRIES:
+    for e in KERNEL_ENTRIES + SPLIT_ENTRIES:
         mangled = f"_Z{len(e)}{e}13FmhaFwdParams"
         assert mangled in syms, mangled
 
@@ -166,6 +168,16 @@ def _mut(**kw):
 ])
 def test_check_rejects(params, batch, causal):
     assert fmha.check_params(params, batch, causal) == INVALID
+
+
+def test_variant_validation():
+    """An unknown kernel form is rejected before anything is launched."""
+    lib = fmha.load_library()
+    p = valid_params()
+    for bad in (-1, 3, 100):
+        assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
+    bad_p = _mut(q=None)
+    assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID
 
 
 def test_null_params_pointer():

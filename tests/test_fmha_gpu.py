@@ -34,10 +34,16 @@ def _report(res):
     return res
 
 
+# both kernel forms behind the launcher: the reference-named entries and the
+# split-KV entries (the launcher's automatic choice is one of the two)
+FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV}
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("row", K_ALL_FULL, ids=[r[0] for r in K_ALL_FULL])
-def test_kallfull_matches_oracle(row):
+def test_kallfull_matches_oracle(row, form):
     prob = problem_from_row(row)
-    res = _report(check_problem(prob, dist="ref", seed=42, rule="reference"))
+    res = _report(check_problem(prob, dist="ref", seed=42, rule="reference", variant=FORMS[form]))
     assert res["pass"], res
 
 
@@ -55,10 +61,11 @@ def test_bshd_causal_gqa_smoke():
     assert res["pass"], res
 
 
+@pytest.mark.parametrize("form", ["auto"] + list(FORMS))
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
-def test_baseline_configs(cfg):
+def test_baseline_configs(cfg, form):
     prob, mult = baseline_problems()[cfg]
-    res = _report(check_baseline(prob, mult))
+    res = _report(check_baseline(prob, mult, variant=fmha.VARIANTS[form]))
     assert res["pass"], res
     if cfg != "cfg5":
         # cfg5 (inputs x2, peaked softmax) is where the reference oracle's own
@@ -67,35 +74,39 @@ def test_baseline_configs(cfg):
         assert res["o_plain"]["pass"], res
 
 
-def test_layout_invariance_bitwise():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_layout_invariance_bitwise(form):
     """BHSD and BSHD storage of the same logical tensors give identical bits."""
     from fmha_native_amd.problem import bhsd_to_bshd
 
     a = Problem(batch=2, nhead_q=4, nhead_k=2, seqlen_q=333, causal=True, lse=True)
     b = Problem(batch=2, nhead_q=4, nhead_k=2, seqlen_q=333, causal=True, lse=True, layout="bshd")
     qa, ka, va = make_inputs(a, "normal", 7)
-    oa, la = run_kernel(a, qa, ka, va)
-    ob, lb = run_kernel(b, bhsd_to_bshd(qa, 2, 4, 333), bhsd_to_bshd(ka, 2, 2, 333), bhsd_to_bshd(va, 2, 2, 333))
+    oa, la = run_kernel(a, qa, ka, va, variant=FORMS[form])
+    ob, lb = run_kernel(b, bhsd_to_bshd(qa, 2, 4, 333), bhsd_to_bshd(ka, 2, 2, 333), bhsd_to_bshd(va, 2, 2, 333),
+                        variant=FORMS[form])
     assert np.array_equal(oa, bshd_to_bhsd(ob, 2, 4, 333))
     assert np.array_equal(la, lb)
 
 
-def test_gqa_equals_replicated_mha_bitwise():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_gqa_equals_replicated_mha_bitwise(form):
     g = Problem(batch=1, nhead_q=8, nhead_k=2, seqlen_q=200, seqlen_k=300, causal=True, lse=True)
     m = Problem(batch=1, nhead_q=8, nhead_k=8, seqlen_q=200, seqlen_k=300, causal=True, lse=True)
     q, k, v = make_inputs(g, "normal", 11)
     rep = lambda t: np.repeat(t.reshape(1, 2, 300, 64), 4, axis=1).reshape(-1)
-    og, lg = run_kernel(g, q, k, v)
-    om, lm = run_kernel(m, q, rep(k), rep(v))
+    og, lg = run_kernel(g, q, k, v, variant=FORMS[form])
+    om, lm = run_kernel(m, q, rep(k), rep(v), variant=FORMS[form])
     assert np.array_equal(og, om)
     assert np.array_equal(lg, lm)
 
 
-def test_varlen_equals_per_sequence_dense_bitwise():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_varlen_equals_per_sequence_dense_bitwise(form):
     seqs = (1, 77, 128, 300, 64, 513)
     pv = Problem(batch=0, nhead_q=4, nhead_k=2, seqlen_q=0, causal=True, lse=True, varlen_seqs=seqs)
     q, k, v = make_inputs(pv, "normal", 5)
-    ov, lv = run_kernel(pv, q, k, v)
+    ov, lv = run_kernel(pv, q, k, v, variant=FORMS[form])
     T = sum(seqs)
     q3, k3, v3 = q.reshape(4, T, 64), k.reshape(2, T, 64), v.reshape(2, T, 64)
     o3, l2 = ov.reshape(4, T, 64), lv.reshape(4, T)
@@ -103,13 +114,14 @@ def test_varlen_equals_per_sequence_dense_bitwise():
     for s in seqs:
         pd = Problem(batch=1, nhead_q=4, nhead_k=2, seqlen_q=s, causal=True, lse=True)
         od, ld = run_kernel(pd, q3[:, start:start + s].reshape(-1), k3[:, start:start + s].reshape(-1),
-                            v3[:, start:start + s].reshape(-1))
+                            v3[:, start:start + s].reshape(-1), variant=FORMS[form])
         assert np.array_equal(od.reshape(4, s, 64), o3[:, start:start + s]), s
         assert np.array_equal(ld.reshape(4, s), l2[:, start:start + s]), s
         start += s
 
 
-def test_masked_and_foreign_keys_contribute_nothing():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_masked_and_foreign_keys_contribute_nothing(form):
     """Keys a row must not see are poisoned (K = 0, so the score is 0 and a
     wrongly included key would get a sizeable weight; V = 16384.0); the
     row's output bits must not change.  (1) the other sequences of a packed varlen batch, (2) the
@@ -119,41 +131,43 @@ def test_masked_and_foreign_keys_contribute_nothing():
     s0 = seqs[0]
     p = Problem(batch=0, nhead_q=2, seqlen_q=0, causal=True, lse=True, varlen_seqs=seqs)
     q, k, v = make_inputs(p, "normal", 9)
-    o1, l1 = run_kernel(p, q, k, v)
+    o1, l1 = run_kernel(p, q, k, v, variant=FORMS[form])
     o1, l1 = o1.reshape(2, T, 64), l1.reshape(2, T)
     big = np.uint16(0x4680)  # bf16 16384.0
 
     k2, v2 = k.reshape(2, T, 64).copy(), v.reshape(2, T, 64).copy()
     k2[:, s0:] = 0
     v2[:, s0:] = big
-    o2, l2 = run_kernel(p, q, k2.reshape(-1), v2.reshape(-1))
+    o2, l2 = run_kernel(p, q, k2.reshape(-1), v2.reshape(-1), variant=FORMS[form])
     assert np.array_equal(o2.reshape(2, T, 64)[:, :s0], o1[:, :s0])
     assert np.array_equal(l2.reshape(2, T)[:, :s0], l1[:, :s0])
 
     k3, v3 = k.reshape(2, T, 64).copy(), v.reshape(2, T, 64).copy()
     k3[:, s0 - 1] = 0  # last key of sequence 0: only its last row may see it
     v3[:, s0 - 1] = big
-    o3, l3 = run_kernel(p, q, k3.reshape(-1), v3.reshape(-1))
+    o3, l3 = run_kernel(p, q, k3.reshape(-1), v3.reshape(-1), variant=FORMS[form])
     assert np.array_equal(o3.reshape(2, T, 64)[:, :s0 - 1], o1[:, :s0 - 1])
     assert np.array_equal(l3.reshape(2, T)[:, :s0 - 1], l1[:, :s0 - 1])
     assert not np.array_equal(o3.reshape(2, T, 64)[:, s0 - 1], o1[:, s0 - 1])
 
 
-def test_stream_and_rerun_bitwise():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_stream_and_rerun_bitwise(form):
     import torch
 
     p = Problem(batch=2, nhead_q=4, seqlen_q=1000, causal=True, lse=True)
     q, k, v = make_inputs(p, "normal", 3)
-    o1, l1 = run_kernel(p, q, k, v)
-    o2, l2 = run_kernel(p, q, k, v)
+    o1, l1 = run_kernel(p, q, k, v, variant=FORMS[form])
+    o2, l2 = run_kernel(p, q, k, v, variant=FORMS[form])
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
-        o3, l3 = run_kernel(p, q, k, v, stream=s.cuda_stream)
+        o3, l3 = run_kernel(p, q, k, v, stream=s.cuda_stream, variant=FORMS[form])
     assert np.array_equal(o1, o2) and np.array_equal(o1, o3)
     assert np.array_equal(l1, l2) and np.array_equal(l1, l3)
 
 
-def test_seqlen_k_zero_gives_zero_and_neg_inf():
+@pytest.mark.parametrize("form", list(FORMS))
+def test_seqlen_k_zero_gives_zero_and_neg_inf(form):
     """No keys at all: O = 0 and LSE = -inf for every row."""
     p = Problem(batch=1, nhead_q=2, seqlen_q=70, seqlen_k=1, lse=True)
     q, k, v = make_inputs(p, "normal", 1)
@@ -168,7 +182,7 @@ def test_seqlen_k_zero_gives_zero_and_neg_inf():
 
     prm = build_params(p, dq, dk, dk, do, dl, None)
     prm.seqlen_k = 0
-    fmha.fmha_fwd_d64_bf16(prm, 1, 0, torch.cuda.current_stream().cuda_stream)
+    fmha.fmha_fwd_d64_bf16(prm, 1, 0, torch.cuda.current_stream().cuda_stream, FORMS[form])
     torch.cuda.synchronize()
     assert np.all(do.cpu().numpy() == 0)
     assert np.all(np.isneginf(dl.cpu().numpy()))
