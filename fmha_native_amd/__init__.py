@@ -25,7 +25,8 @@ import numpy as np
 __all__ = [
     "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
     "tile_config", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
-    "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANTS",
+    "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
+    "VARIANTS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -96,8 +97,8 @@ def load_library(path=LIB_PATH):
     return lib
 
 
-VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV = 0, 1, 2
-VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV}
+VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR = 0, 1, 2, 3
+VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):

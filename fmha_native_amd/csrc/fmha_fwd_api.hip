@@ -74,12 +74,14 @@ int device_cus() {
 
 // The split-KV entries give each M-tile twice the waves (two 4-wave groups
 // per block, one block per CU), each walking half of its key range.  They pay
-// off when the regular grid leaves compute units short of work: measured on
-// MI355X, +12-16% at 128-256 blocks, even at ~600, -4% at 1024.
-bool use_splitkv(int blocks) {
-    if (FMHA_SPLIT_POLICY == 0) return false;
-    if (FMHA_SPLIT_POLICY == 1) return true;
-    return blocks <= 2 * device_cus();
+// off when the regular grid (two resident blocks per CU) leaves compute units
+// short of work.  Measured on MI355X (256 CUs): +12-16% at 128-256 blocks,
+// +2% at 626, -4% at 1024.  The pair entries are never picked automatically
+// (within a few % of the regular entries either way).
+int pick_variant(int blocks) {
+    if (FMHA_SPLIT_POLICY == 0) return FMHA_VARIANT_REGULAR;
+    if (FMHA_SPLIT_POLICY == 1) return FMHA_VARIANT_SPLITKV;
+    return blocks < 3 * device_cus() ? FMHA_VARIANT_SPLITKV : FMHA_VARIANT_REGULAR;
 }
 
 }  // namespace
@@ -88,14 +90,29 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
                                                 hipStream_t stream) {
     const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
     if (chk != hipSuccess) return chk;
-    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SPLITKV) return hipErrorInvalidValue;
+    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_PAIR) return hipErrorInvalidValue;
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
     const bool varlen = p->seqstart_q != nullptr;
-    const bool split = variant == FMHA_VARIANT_AUTO ? use_splitkv(p->nhead_q * m_tiles * batch)
-                                                     : variant == FMHA_VARIANT_SPLITKV;
-    if (split) {
+    if (variant == FMHA_VARIANT_AUTO) variant = pick_variant(p->nhead_q * m_tiles * batch);
+    if (variant == FMHA_VARIANT_PAIR) {
+        const dim3 pgrid(p->nhead_q, (m_tiles + 1) / 2, batch);
+        const dim3 block(FMHA_SPLIT_KBLOCK);
+        if (varlen) {
+            if (causal)
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk1_varlen, pgrid, block, 0, stream, *p);
+            else
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk0_varlen, pgrid, block, 0, stream, *p);
+        } else {
+            if (causal)
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk1, pgrid, block, 0, stream, *p);
+            else
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk0, pgrid, block, 0, stream, *p);
+        }
+        return hipGetLastError();
+    }
+    if (variant == FMHA_VARIANT_SPLITKV) {
         const dim3 block(FMHA_SPLIT_KBLOCK);
         if (varlen) {
             if (causal)

@@ -170,19 +170,30 @@ struct Softmax {
     float l_tile;  // this lane's sum of P over the current tile
 };
 
-// One block = one kTileM-row M-tile of (batch b, head h), computed by kSplit
-// groups of kWaves waves.  Group g walks the g-th contiguous share of the
-// M-tile's key tiles with its own half of every LDS stage; with kSplit = 2
-// the groups' partial (O^T, m, l) are merged through LDS at the end (group 1
-// hands over, group 0 writes O and LSE).  All groups run the same number of
+// Block forms.  Every group of kWaves waves computes 128 query rows over a
+// range of key tiles; all groups of a block run the same number of
 // iterations, so the block-wide barriers stay in step.
-template <bool kCausal, bool kVarlen, int kSplit>
+//  * kModeRegular: one group, one M-tile (the reference's entries).
+//  * kModeSplitKV: two groups on the same M-tile, each walking a contiguous
+//    half of its key tiles with its own half of every LDS stage; their
+//    partial (O^T, m, l) are merged through LDS at the end (group 1 hands
+//    over, group 0 writes O and LSE).  For grids too small to fill the GPU.
+//  * kModePair: two groups on the adjacent M-tiles 2mt and 2mt+1 of one
+//    (batch, head), sharing every K/V tile (loaded once, by all 8 waves).
+//    The shared barrier keeps both in lockstep: two separate blocks on one
+//    compute unit progress unevenly (one is served first), so the CU's last
+//    block runs alone at the end; a pair has no such tail.
+enum : int { kModeRegular = 0, kModeSplitKV = 1, kModePair = 2 };
+template <bool kCausal, bool kVarlen, int kMode>
 __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, const Ring& ring) {
-    static_assert(kSplit == 1 || kSplit == 2, "one or two key-range groups per block");
+    constexpr int kGroups = kMode == kModeRegular ? 1 : 2;
+    constexpr bool kSplitKV = kMode == kModeSplitKV;
+    constexpr bool kPair = kMode == kModePair;
+    constexpr int kLoads = kPair ? 1 : kLoadsPerTile;  // DMA loads per wave, tensor and tile
     const int lane = threadIdx.x & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int group = kSplit == 1 ? 0 : wave_id / kWaves;                  // key-range group
-    const int wave = kSplit == 1 ? wave_id : wave_id % kWaves;             // wave within the group
+    const int group = kGroups == 1 ? 0 : wave_id / kWaves;
+    const int wave = kGroups == 1 ? wave_id : wave_id % kWaves;            // wave within the group
     const int l32 = lane & 31;
     const int hi = lane >> 5;
 
@@ -198,8 +209,9 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         sq = p.seqlen_q;
         sk = p.seqlen_k;
     }
-    const int row0 = mt * kTileM;
-    if (row0 >= sq) return;  // varlen: this M-tile is past the sequence
+    const int blk_row0 = (kPair ? 2 * mt : mt) * kTileM;  // the block's first row
+    if (blk_row0 >= sq) return;  // varlen: this M-tile is past the sequence
+    const int row0 = blk_row0 + (kPair ? group * kTileM : 0);  // this group's M-tile
     const int kvh = h / (p.nhead_q / p.nhead_k);
 
     const __bf16* qbase;
@@ -231,7 +243,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int shift = sk - sq;
     int kv_end = sk;
     if constexpr (kCausal) {
-        int last = row0 + kTileM - 1;
+        int last = blk_row0 + (kPair ? 2 : 1) * kTileM - 1;
         if (last > sq - 1) last = sq - 1;
         int e = last + shift + 1;
         kv_end = e < 0 ? 0 : (e > sk ? sk : e);
@@ -239,8 +251,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int ntiles = (kv_end + kTileN - 1) / kTileN;
     // this group's key tiles: global tiles [tile0, tile0 + ntg) (the loops
     // below count group-local tiles 0 .. ntg-1); tiles >= tile_end are dead
-    const int ntg = (ntiles + kSplit - 1) / kSplit;
-    const int tile0 = group * ntg;
+    const int ntg = kSplitKV ? (ntiles + 1) / 2 : ntiles;
+    const int tile0 = kSplitKV ? group * ntg : 0;
     const int tile_end = min(ntiles, tile0 + ntg);
 
     const int wrow0 = row0 + wave * kRowsPerWave;  // first query row of this wave
@@ -261,12 +273,14 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
     }
 
-    // ---- global -> LDS tile loaders: per tile each wave moves 2 x 1 KiB of
-    // K (or V).  Lane L of load i writes LDS row 8*(2*wave+i) + L/8, physical
-    // chunk L%8, fetched from logical chunk (L%8) ^ swz(row).  Tiles past the
-    // KV range get an empty descriptor (zero fill, no memory traffic), so
-    // every iteration issues the same number of loads. ----
-    const int ld_row = (2 * wave) * 8 + (lane >> 3);
+    // ---- global -> LDS tile loaders: per tile each wave moves kLoads x 1 KiB
+    // of K (or V).  Lane L of load i writes LDS row 8*(kLoads*w+i) + L/8
+    // (w: the wave's index among the waves sharing the tile), physical chunk
+    // L%8, fetched from logical chunk (L%8) ^ swz(row).  Tiles past the KV
+    // range get an empty descriptor (zero fill, no memory traffic), so every
+    // iteration issues the same number of loads. ----
+    const int ld_wave = kPair ? wave_id : wave;
+    const int ld_row = (kLoads * ld_wave) * 8 + (lane >> 3);
     const int ld_pc = lane & 7;
     const int k_ld_off0 = ld_row * p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row)) << 4);
     const int k_ld_off1 = (ld_row + 8) * p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row + 8)) << 4);
@@ -274,8 +288,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int v_ld_off1 = (ld_row + 8) * p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row + 8)) << 4);
     const int k_tile_step = kTileN * p.stride_k * 2;
     const int v_tile_step = kTileN * p.stride_v * 2;
-    const int goff = group * kTileBytes;  // this group's half of every LDS stage
-    const int wave_off = goff + (2 * wave) * 1024;
+    const int goff = kSplitKV ? group * kTileBytes : 0;  // split-KV: this group's half of every stage
+    const int wave_off = goff + (kLoads * ld_wave) * 1024;
 
     // Local tile t's K lands in K stage t % kRing, its V in V stage t % kRing.
     // The tile's own descriptor (base at the tile's first row, num_records =
@@ -287,7 +301,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         const uint32_t t0 = (uint32_t)gt * (uint32_t)k_tile_step;
         const auto r = make_rsrc((const char*)kbase + t0, gt < tile_end ? kbytes - t0 : 0u);
         lds_dma_16(r, dst, k_ld_off0);
-        lds_dma_16(r, dst + 1024, k_ld_off1);
+        if constexpr (kLoads == 2) lds_dma_16(r, dst + 1024, k_ld_off1);
     };
     auto issue_v = [&](int tile, auto stage_c) {
         lds_char* dst = ring.v[decltype(stage_c)::value] + wave_off;
@@ -295,7 +309,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         const uint32_t t0 = (uint32_t)gt * (uint32_t)v_tile_step;
         const auto r = make_rsrc((const char*)vbase + t0, gt < tile_end ? vbytes - t0 : 0u);
         lds_dma_16(r, dst, v_ld_off0);
-        lds_dma_16(r, dst + 1024, v_ld_off1);
+        if constexpr (kLoads == 2) lds_dma_16(r, dst + 1024, v_ld_off1);
     };
 
     // ---- per-lane LDS read offsets inside a tile ----
@@ -454,7 +468,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         constexpr int cur = J & 1, nxt = cur ^ 1;
         // K(t+1) and V(t-1) were fetched three iterations ago; the loads of
         // the two previous iterations may still fly.
-        vmcnt_wait<4 * kLoadsPerTile>();
+        vmcnt_wait<4 * kLoads>();
         __syncthreads();
         issue_k(t + kRing, std::integral_constant<int, J>{});
         issue_v(t + 2, std::integral_constant<int, (J + 2) % kRing>{});
@@ -484,11 +498,13 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         for (int i = 0; i < 4; ++i) pbuf[1][i] = bf16x8{};
         {
             typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
-            static_assert(kTileBytes == 2 * kGroupSize * 16, "two 16-byte stores per thread zero a stage");
+            // the threads sharing the stage region (a group, or the whole pair)
+            constexpr int kRegionThreads = kPair ? 2 * kGroupSize : kGroupSize;
+            static_assert(kTileBytes % (16 * kRegionThreads) == 0, "whole 16-byte stores per thread");
             lds_i32x4* z = (lds_i32x4*)(ring.v[kRing - 1] + goff);
-            const int tig = threadIdx.x % kGroupSize;
-            z[tig] = i32x4{};
-            z[tig + kGroupSize] = i32x4{};
+            const int tir = kPair ? (int)threadIdx.x : (int)threadIdx.x % kGroupSize;
+#pragma unroll
+            for (int i = 0; i < kTileBytes / (16 * kRegionThreads); ++i) z[tir + i * kRegionThreads] = i32x4{};
         }
         // prologue: K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once K0 landed
         issue_k(0, P0{});
@@ -497,7 +513,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_k(2, P2{});
         issue_v(1, P1{});
         issue_k(3, P3{});
-        vmcnt_wait<5 * kLoadsPerTile>();
+        vmcnt_wait<5 * kLoads>();
         __syncthreads();
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
@@ -531,7 +547,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         }
     }
 
-    if constexpr (kSplit == 2) {
+    if constexpr (kSplitKV) {
         // Hand-over: group 1 leaves its partial (O^T, m_ref, l_part) in LDS and
         // exits; group 0 folds it into its own.  The K stages are free: their
         // last reads (GEMM0 of the final iteration) completed before the
@@ -542,7 +558,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         // chain: a runtime-indexed table of LDS addresses cannot be emitted)
         lds_char* xs = wave == 0 ? ring.k[0] : wave == 1 ? ring.k[1] : wave == 2 ? ring.k[2] : ring.k[3];
         lds_float* x = (lds_float*)xs;
-        static_assert(34 * 64 * 4 <= kSplit * kTileBytes, "hand-over fits one K stage");
+        static_assert(34 * 64 * 4 <= 2 * kTileBytes, "hand-over fits one K stage");
         if (group == 1) {
 #pragma unroll
             for (int db = 0; db < 2; ++db)
@@ -616,19 +632,19 @@ static_assert(kRing == 4, "FMHA_RING declares four stages per ring");
 
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
-    fwd_mtile<false, false, 1>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    fwd_mtile<false, false, kModeRegular>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
-    fwd_mtile<true, false, 1>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    fwd_mtile<true, false, kModeRegular>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk0_varlen(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
-    fwd_mtile<false, true, 1>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    fwd_mtile<false, true, kModeRegular>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
-    fwd_mtile<true, true, 1>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    fwd_mtile<true, true, kModeRegular>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
 
 // ---- split-KV entries (this build's own; no counterpart in the reference):
@@ -641,17 +657,37 @@ static_assert(FMHA_SPLIT_KBLOCK == 2 * FMHA_KBLOCK, "two groups of kBlockSize th
 
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk0(FmhaFwdParams params) {
     FMHA_RING(ring, 2 * kTileBytes)
-    fwd_mtile<false, false, 2>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    fwd_mtile<false, false, kModeSplitKV>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1(FmhaFwdParams params) {
     FMHA_RING(ring, 2 * kTileBytes)
-    fwd_mtile<true, false, 2>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    fwd_mtile<true, false, kModeSplitKV>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk0_varlen(FmhaFwdParams params) {
     FMHA_RING(ring, 2 * kTileBytes)
-    fwd_mtile<false, true, 2>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+    fwd_mtile<false, true, kModeSplitKV>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
 }
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1_varlen(FmhaFwdParams params) {
     FMHA_RING(ring, 2 * kTileBytes)
-    fwd_mtile<true, true, 2>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+    fwd_mtile<true, true, kModeSplitKV>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+}
+
+// ---- pair entries (this build's own; no counterpart in the reference):
+// grid (nhead_q, ceil(ceil(seqlen_q/kM0)/2), batch), 2*kBlockSize threads;
+// block y owns M-tiles 2y and 2y+1 (causal: heaviest pairs first). ----
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk0(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<false, false, kModePair>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, false, kModePair>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk0_varlen(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<false, true, kModePair>(params, blockIdx.z, blockIdx.x, blockIdx.y, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, true, kModePair>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }

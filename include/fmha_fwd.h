@@ -103,7 +103,7 @@ typedef struct FmhaFwdParams {
  * Returns hipSuccess, hipErrorInvalidValue for rejected arguments (nothing is
  * launched), or the launch error.  Asynchronous like any kernel launch; it
  * allocates nothing (its only state is a per-device cache of the compute-unit
- * count), so concurrent calls are safe.  Grids with at most 2 blocks per
+ * count), so concurrent calls are safe.  Grids with fewer than 3 blocks per
  * compute unit run the split-KV form (see fmha_fwd_d64_bf16_variant).
  * Replaces src/bench_fmha_fwd.cpp:174-191. */
 hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
@@ -112,14 +112,17 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 /* The same launch with the kernel form chosen by the caller (this build's
  * own; no counterpart in the reference):
  *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: split-KV when the
- *                         grid has at most 2 blocks per compute unit
+ *                         grid has fewer than 3 blocks per compute unit
  *   FMHA_VARIANT_REGULAR  the four reference-named entries (kBlockSize threads)
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
+ *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
+ *                         per two adjacent M-tiles of a (batch, head)
  * Both forms give the same results up to fp32 rounding order.  An unknown
  * variant returns hipErrorInvalidValue. */
 #define FMHA_VARIANT_AUTO 0
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
+#define FMHA_VARIANT_PAIR 3
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
 
@@ -167,6 +170,13 @@ __global__ void fmha_fwd_d64_bf16_splitkv_msk0(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_splitkv_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_splitkv_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_splitkv_msk1_varlen(FmhaFwdParams params);
+/* Pair forms (no counterpart in the reference): grid (nhead_q,
+ * ceil(ceil(seqlen_q/kM0)/2), batch), block FMHA_SPLIT_KBLOCK; block y
+ * computes M-tiles 2y and 2y+1 with one shared K/V stream. */
+__global__ void fmha_fwd_d64_bf16_pair_msk0(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_pair_msk1(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_pair_msk0_varlen(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params);
 #endif
 #endif /* __cplusplus */
 

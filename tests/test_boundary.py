@@ -28,8 +28,8 @@ REFERENCE_OFFSETS = {
 }
 KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_d64_bf16_msk0_varlen",
                   "fmha_fwd_d64_bf16_msk1_varlen"]
-SPLIT_ENTRIES = ["fmha_fwd_d64_bf16_splitkv_msk0", "fmha_fwd_d64_bf16_splitkv_msk1",
-                 "fmha_fwd_d64_bf16_splitkv_msk0_varlen", "fmha_fwd_d64_bf16_splitkv_msk1_varlen"]
+SPLIT_ENTRIES = [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("splitkv", "pair") for m in (0, 1)
+                 for v in ("", "_varlen")]
 
 
 def header_c_functions():
@@ -174,7 +174,7 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    for bad in (-1, 3, 100):
+    for bad in (-1, 4, 100):  # 0-3 are the valid forms
         assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
     bad_p = _mut(q=None)
     assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID

@@ -34,9 +34,9 @@ def _report(res):
     return res
 
 
-# both kernel forms behind the launcher: the reference-named entries and the
-# split-KV entries (the launcher's automatic choice is one of the two)
-FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV}
+# every kernel form behind the launcher: the reference-named entries, the
+# split-KV entries and the pair entries (the automatic choice is one of them)
+FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR}
 
 
 @pytest.mark.parametrize("form", list(FORMS))
