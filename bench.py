@@ -38,20 +38,23 @@ def _problems():
     return cfg2, cfg3
 
 
-def _device_inputs(prob, torch, seed=42):
+def _device_inputs(prob, torch, seed=42, mult=1.0):
     import numpy as np
 
     import fmha_native_amd as fmha
 
     nq, nk, nlse = prob.sizes()
-    host = (fmha.fill_normal(seed, nq), fmha.fill_normal(seed + 1, nk), fmha.fill_normal(seed + 2, nk))
+    host = (fmha.fill_normal(seed, nq, mult), fmha.fill_normal(seed + 1, nk, mult),
+            fmha.fill_normal(seed + 2, nk, mult))
     dev = [torch.from_numpy(a.view(np.int16)).to("cuda:0") for a in host]
     o = torch.empty(nq, dtype=torch.int16, device="cuda:0")
     lse = torch.empty(nlse, dtype=torch.float32, device="cuda:0") if prob.lse else None
-    return host, dev, o, lse
+    ss = prob.seqstart()
+    seq = torch.from_numpy(ss).to("cuda:0") if ss is not None else None
+    return host, dev, o, lse, seq
 
 
-def _params(prob, dq, dk, dv, do, dlse):
+def _params(prob, dq, dk, dv, do, dlse, dseq=None):
     import fmha_native_amd as fmha
 
     p = fmha.FmhaFwdParams()
@@ -65,16 +68,18 @@ def _params(prob, dq, dk, dv, do, dlse):
         setattr(p, f"stride_{t}", s)
         setattr(p, f"nhead_stride_{t}", hs)
         setattr(p, f"batch_stride_{t}", bs)
+    if dseq is not None:
+        p.seqstart_q = p.seqstart_k = dseq.data_ptr()
     return p
 
 
-def time_problem(prob, steps, warmup, torch):
+def time_problem(prob, steps, warmup, torch, mult=1.0):
     """Warm up, then time exactly `steps` back-to-back launches on torch's
     current stream with HIP events recorded on that same stream."""
     import fmha_native_amd as fmha
 
-    host, (dq, dk, dv), do, dlse = _device_inputs(prob, torch)
-    p = _params(prob, dq, dk, dv, do, dlse)
+    host, (dq, dk, dv), do, dlse, dseq = _device_inputs(prob, torch, mult=mult)
+    p = _params(prob, dq, dk, dv, do, dlse, dseq)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     for _ in range(warmup):
@@ -168,6 +173,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
     ap.add_argument("--only", choices=["cfg2", "cfg3"], help="time one workload only (profiling runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run `steps` device-to-device copies of this many MiB (HBM counter calibration)")
@@ -201,6 +207,24 @@ def main():
         return
     r2 = time_problem(cfg2, args.steps, args.warmup, torch)
     r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)
+    # the other benchmark configurations, reported beside the headline
+    others = {}
+    if not args.no_extra:
+        from fmha_native_amd.problem import baseline_problems
+
+        for name in ("cfg1", "cfg4", "cfg5"):
+            prob, mult = baseline_problems()[name]
+            r = time_problem(prob, max(1, args.steps // 4), max(1, args.warmup // 2), torch, mult)
+            e = {"workload": prob.name, "ms_per_step": round(r["ms"], 5), "value": round(r["tflops"], 2),
+                 "pct_bf16_peak": round(100.0 * r["tflops"] / PEAK_BF16_TFLOPS, 2)}
+            if prob.varlen:
+                e["value_exact_flops"] = round(prob.exact_flops() / (r["ms"] * 1e-3) / 1e12, 2)
+                e["note"] = ("value uses the repo FLOP convention (max S for every sequence, an overcount); "
+                             "value_exact_flops counts the visible (q, k) pairs")
+            if name == "cfg1":
+                e["hbm_gbs"] = round(prob.io_bytes() / (r["ms"] * 1e-3) / 1e9, 1)
+                e["note"] = "launch-latency bound; hbm_gbs = algorithmic bytes / time"
+            others[name] = e
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -240,6 +264,7 @@ def main():
             "pct_bf16_peak": round(100.0 * r3["tflops"] / PEAK_BF16_TFLOPS, 2),
             "vs_reference_mi300x": round(r3["tflops"] / 358.1, 3),
         },
+        "others": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

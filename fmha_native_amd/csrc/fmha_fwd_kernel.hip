@@ -34,9 +34,11 @@
 //  * Softmax in the exp2 domain with the log2(e) already folded into scale
 //    (as the reference, params.hpp:38-43), speculative: P is computed in the
 //    current reference-max frame without taking the tile's max; only when a
-//    lane's tile sum of P exceeds 256 (so some score is far above the frame)
+//    lane's tile sum of P exceeds 2^16 (so some score is far above the frame)
 //    does the wave take the exact max, rescale O^T and l, and redo the tile.
-//    Any frame gives the same O and LSE; this one keeps every P <= 256.
+//    Any frame gives the same O and LSE; this one keeps every P <= 2^16
+//    (far inside fp32 and bf16 range), and a frame lasts until a row's max
+//    grows by more than ~11 (log2 units) past it.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -62,7 +64,10 @@ constexpr int kRowBytes = 128;                 // 64 bf16 per K/V row in LDS
 constexpr int kTileBytes = kTileN * kRowBytes; // 8 KiB
 constexpr int kRing = 4;                       // stages per ring (K and V)
 constexpr int kLoadsPerTile = 2;                   // 1 KiB DMA per load, per wave
-constexpr float kGrowSum = 256.0f;                 // tile-sum bound of the speculative softmax
+#ifndef FMHA_GROW_SUM
+#define FMHA_GROW_SUM 65536.0f
+#endif
+constexpr float kGrowSum = FMHA_GROW_SUM;          // tile-sum bound of the speculative softmax
 constexpr float kMaxSeed = -5000.0f;               // raw-score running max seed (pipeline.hpp:248-252)
 constexpr uint32_t kBufferWord3 = 0x00020000u;     // raw dword buffer, gfx9 family
 

@@ -126,3 +126,23 @@ def bhsd_to_bshd(a, b, h, s, d=HEAD_DIM):
 
 def bshd_to_bhsd(a, b, h, s, d=HEAD_DIM):
     return np.ascontiguousarray(np.asarray(a).reshape(b, s, h, d).transpose(0, 2, 1, 3)).reshape(-1)
+
+
+def baseline_problems(varlen_seed=42):
+    """The five benchmark configurations as {name: (Problem, input multiplier)}:
+    cfg1 B1 H2 S128 (+LSE), cfg2 B4 H16 S2048 dense, cfg3 B1 H16 S8192 causal
+    (+LSE), cfg4 eight varlen sequences U[128, 4096] causal (+LSE), cfg5 B1 H2
+    S40000 causal (+LSE) with inputs x2.  Inputs are N(0,1) (seed 42)."""
+    from fmha_native_amd import varlen_lengths
+
+    lens = varlen_lengths(varlen_seed, 8, 128, 4096)
+    return {
+        "cfg1": (Problem(batch=1, nhead_q=2, seqlen_q=128, lse=True, name="cfg1_B1H2S128"), 1.0),
+        "cfg2": (Problem(batch=4, nhead_q=16, seqlen_q=2048, name="cfg2_B4H16S2048"), 1.0),
+        "cfg3": (Problem(batch=1, nhead_q=16, seqlen_q=8192, causal=True, lse=True, name="cfg3_B1H16S8192_causal"),
+                 1.0),
+        "cfg4": (Problem(batch=8, nhead_q=16, seqlen_q=0, causal=True, lse=True, varlen_seqs=tuple(lens),
+                         name="cfg4_varlen8_causal"), 1.0),
+        "cfg5": (Problem(batch=1, nhead_q=2, seqlen_q=40000, causal=True, lse=True,
+                         name="cfg5_B1H2S40000_causal_x2"), 2.0),
+    }

@@ -100,17 +100,4 @@ def all_full():
 
 
 # Benchmark configurations (inputs N(0,1) unless noted; seed 42).
-def baseline_problems(varlen_seed=42):
-    from fmha_native_amd import varlen_lengths
-
-    lens = varlen_lengths(varlen_seed, 8, 128, 4096)
-    return {
-        "cfg1": (Problem(batch=1, nhead_q=2, seqlen_q=128, lse=True, name="cfg1_B1H2S128"), 1.0),
-        "cfg2": (Problem(batch=4, nhead_q=16, seqlen_q=2048, name="cfg2_B4H16S2048"), 1.0),
-        "cfg3": (Problem(batch=1, nhead_q=16, seqlen_q=8192, causal=True, lse=True, name="cfg3_B1H16S8192_causal"),
-                 1.0),
-        "cfg4": (Problem(batch=8, nhead_q=16, seqlen_q=0, causal=True, lse=True, varlen_seqs=tuple(lens),
-                         name="cfg4_varlen8_causal"), 1.0),
-        "cfg5": (Problem(batch=1, nhead_q=2, seqlen_q=40000, causal=True, lse=True,
-                         name="cfg5_B1H2S40000_causal_x2"), 2.0),
-    }
+from fmha_native_amd.problem import baseline_problems  # noqa: E402,F401
