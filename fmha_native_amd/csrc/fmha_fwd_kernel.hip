@@ -105,6 +105,22 @@ template <int N>
 __device__ __forceinline__ void vmcnt_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Workgroup barrier of the K/V ring, without __syncthreads()'s memory fence:
+// that fence waits vmcnt(0), i.e. also for the prefetches still in flight.
+// What the barrier publishes is already complete: each wave waited for its
+// own DMA of the tile (vmcnt_wait) and for its own LDS reads of the stage
+// about to be refilled (their MFMAs consumed them).  The "memory" clobber
+// keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// A copy of a wave-uniform value in a VGPR.  A VALU operand read from an SGPR
+// costs gfx950 ~4.4 issue cycles per wave64 instruction against ~2.6-3.2 for
+// VGPR operands (fma, mul, sub alike), so per-element operands are kept in VGPRs.
+__device__ __forceinline__ float in_vgpr(float x) {
+    float v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(x));
+    return v;
+}
 
 // XOR swizzle of the 16-byte chunk index inside a 128-byte K row (row & 15 is
 // all it depends on).  Conflict-free ds_read_b128 for both 32- and 64-bank LDS.
@@ -341,7 +357,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         }
     }
 
-    const float scale = p.scale;  // log2(e)/sqrt(D)
+    const float scale = p.scale;          // log2(e)/sqrt(D)
+    const float scale_v = in_vgpr(scale);  // the per-score fma's operand
     Softmax sm{kMaxSeed, 0.0f, 0.0f};
     constexpr int kGroupSize = kWaves * 64;  // threads per key-range group
     f32x16 oacc[2];
@@ -386,7 +403,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             const int d = lim - (key0 + 4 * hi);
             const uint32_t lo = d < 0 ? 0u : (d >= 31 ? 0xffffffffu : (2u << d) - 1u);
             const uint32_t hi_bits = d < 32 ? 0u : (d >= 63 ? 0xffffffffu : (2u << (d - 32)) - 1u);
-            const uint32_t ninf = 0xff800000u;
+            const uint32_t ninf = __float_as_uint(in_vgpr(-__builtin_inff()));
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -418,11 +435,11 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 bf16x8 pk;
-                float acc = 0.0f;
+                float acc;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 * k + e], scale, neg_ms));
-                    acc += pv;
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 * k + e], scale_v, neg_ms));
+                    acc = e == 0 ? pv : acc + pv;
                     pk[e] = (__bf16)pv;
                 }
                 ls[2 * kb + k] = acc;
@@ -474,7 +491,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         // K(t+1) and V(t-1) were fetched three iterations ago; the loads of
         // the two previous iterations may still fly.
         vmcnt_wait<4 * kLoads>();
-        __syncthreads();
+        ring_barrier();
         issue_k(t + kRing, std::integral_constant<int, J>{});
         issue_v(t + 2, std::integral_constant<int, (J + 2) % kRing>{});
         mask_tile(t, sacc[cur]);
@@ -488,7 +505,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     auto last_gemm1 = [&](auto phase_c) {
         constexpr int J = decltype(phase_c)::value;
         vmcnt_wait<0>();  // every DMA landed (none may outlive the block)
-        __syncthreads();
+        ring_barrier();
         gemm1(std::integral_constant<int, J>{}, pbuf[J & 1]);
     };
     using P0 = std::integral_constant<int, 0>;
@@ -519,7 +536,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_v(1, P1{});
         issue_k(3, P3{});
         vmcnt_wait<5 * kLoads>();
-        __syncthreads();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the zeroing stores above
+        ring_barrier();
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
         // speculative softmax holds from tile 0 on (rows with no visible key
