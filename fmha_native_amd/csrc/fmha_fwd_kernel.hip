@@ -107,11 +107,14 @@ __device__ __forceinline__ void vmcnt_wait() {
 }
 // Workgroup barrier of the K/V ring, without __syncthreads()'s memory fence:
 // that fence waits vmcnt(0), i.e. also for the prefetches still in flight.
-// What the barrier publishes is already complete: each wave waited for its
-// own DMA of the tile (vmcnt_wait) and for its own LDS reads of the stage
-// about to be refilled (their MFMAs consumed them).  The "memory" clobber
-// keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// Before the barrier each wave has waited for its own DMA of the tile about
+// to be read (vmcnt_wait) and, here, for all of its own LDS reads
+// (lgkmcnt(0)): right after the barrier other waves refill the stages those
+// reads came from, and s_barrier itself waits for no memory operation (the
+// compiler may otherwise leave a read in flight across it when it sinks the
+// consuming MFMA past the barrier).  The "memory" clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // A copy of a wave-uniform value in a VGPR.  A VALU operand read from an SGPR
 // costs gfx950 ~4.4 issue cycles per wave64 instruction against ~2.6-3.2 for
@@ -536,8 +539,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_v(1, P1{});
         issue_k(3, P3{});
         vmcnt_wait<5 * kLoads>();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the zeroing stores above
-        ring_barrier();
+        ring_barrier();  // also completes the zeroing stores above (lgkmcnt)
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
         // speculative softmax holds from tile 0 on (rows with no visible key

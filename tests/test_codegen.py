@@ -1,0 +1,68 @@
+"""Static checks of the gfx950 code the kernel source compiles to (CPU only).
+
+The K/V ring's barrier is a bare s_barrier (no memory fence), so the
+property it relies on is checked on the generated code itself: at every
+s_barrier of every entry, the wave has no LDS read in flight (an
+``s_waitcnt lgkmcnt(0)`` follows the last ds_read).  A read left in flight
+would race with the other waves' DMA refill of its stage right after the
+barrier.  Also: no entry spills to scratch, and every entry keeps two waves
+per SIMD.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from fmha_native_amd import build
+
+_ENTRIES = [f"fmha_fwd_d64_bf16_{form}msk{m}{v}" for form in ("", "splitkv_", "pair_")
+            for m in (0, 1) for v in ("", "_varlen")]
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    if shutil.which(build.HIPCC) is None and not os.path.exists(build.HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "kernel.s"
+    cmd = [build.HIPCC, *[f for f in build.HIP_FLAGS if f != "-fPIC"], "--cuda-device-only", "-S",
+           os.path.join(build.CSRC, "fmha_fwd_kernel.hip"), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    return out.read_text()
+
+
+def _functions(src):
+    funcs = {}
+    for m in re.finditer(r"^(_Z[^\s:]+):", src, re.M):
+        end = src.index(".Lfunc_end", m.end())
+        funcs[m.group(1)] = src[m.end():end]
+    return funcs
+
+
+def test_every_entry_compiled(asm):
+    names = _functions(asm)
+    for e in _ENTRIES:
+        assert any(e + "13FmhaFwdParams" in n for n in names), e
+
+
+def test_no_lds_read_in_flight_at_barriers(asm):
+    for name, body in _functions(asm).items():
+        pending, barriers = False, 0
+        for line in body.splitlines():
+            ins = line.strip()
+            if ins.startswith("ds_read"):
+                pending = True
+            elif re.match(r"s_waitcnt\b.*lgkmcnt\(0\)", ins):
+                pending = False
+            elif ins.startswith("s_barrier"):
+                barriers += 1
+                assert not pending, f"{name}: LDS read in flight at barrier {barriers}"
+        assert barriers > 0, name
+
+
+def test_no_scratch_and_two_waves_per_simd(asm):
+    scratch = re.findall(r"; ScratchSize: (\d+)", asm)
+    occupancy = re.findall(r"; Occupancy: (\d+)", asm)
+    assert scratch and all(int(s) == 0 for s in scratch), scratch
+    assert occupancy and all(int(o) >= 2 for o in occupancy), occupancy

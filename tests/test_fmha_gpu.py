@@ -186,3 +186,38 @@ def test_seqlen_k_zero_gives_zero_and_neg_inf(form):
     torch.cuda.synchronize()
     assert np.all(do.cpu().numpy() == 0)
     assert np.all(np.isneginf(dl.cpu().numpy()))
+
+
+def _to_bf16_bits(x):
+    """float32 -> bf16 bits, round to nearest even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("causal,lse", [(False, False), (False, True), (True, True)])
+def test_growing_row_max_reframes(form, causal, lse):
+    """Scores that rise by ~16 (raw) per 64-key tile: a row's max keeps growing
+    past the frame the speculative softmax started from, so the kernel's
+    re-framing path (exact max, rescale of O and l, recomputed P) runs every
+    few tiles.  Heads 0 and 2 grow, heads 1 and 3 are plain N(0,1)."""
+    p = Problem(batch=2, nhead_q=4, seqlen_q=1000, causal=causal, lse=lse)
+    rng = np.random.default_rng(17)
+    shape = (2, 4, 1000, 64)
+    q = rng.standard_normal(shape, dtype=np.float32)
+    k = rng.standard_normal(shape, dtype=np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    ramp = (np.arange(1000) // 64).astype(np.float32) / 4.0  # + 0.25 per tile in every dim
+    for h in (0, 2):
+        q[:, h] = 1.0
+        k[:, h] = ramp[None, :, None] + 0.125 * k[:, h]
+    qb, kb, vb = (_to_bf16_bits(t).reshape(-1) for t in (q, k, v))
+    o_bits, lse_k = run_kernel(p, qb, kb, vb, variant=FORMS[form])
+    o_ref, lse_ref = oracle.run(p, qb, kb, vb, p_trunc=False)
+    res = {"o": verify.baseline_rule(o_ref, verify.bf16_bits_to_f32(o_bits))}
+    if lse:
+        res["lse"] = verify.lse_rule(lse_ref, lse_k)
+    _report(res)
+    assert res["o"]["pass"], res
+    if lse:
+        assert res["lse"]["pass"], res
