@@ -157,12 +157,14 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Schedule of one pipelined iteration: 16 slots of {1 MFMA, the DS reads of
-// the MFMA kDsAhead slots later, kValuPerSlot VALU}.  MFMAs 0-7 are GEMM1's
-// (two tr_b16 reads each), 8-15 GEMM0's (one b128 read each); the reads of
-// MFMAs 0 .. kDsAhead-1 open the iteration.  Groups are filled in order,
-// respecting dependences.  The softmax of a tile is ~117 VALU (32 fma, 32
-// exp, 35 add, 16 cvt_pk, bookkeeping), spread evenly over the 16 MFMAs.
+// Schedule of one pipelined iteration: one slot per MFMA of {1 MFMA, the DS
+// reads of the MFMA kDsAhead slots later, VALU}.  A full iteration has 16
+// MFMAs: 0-7 GEMM1's (two tr_b16 reads each), 8-15 GEMM0's (one b128 read
+// each).  The first iteration of a block has no GEMM1 (there is no tile -1)
+// and the last no GEMM0 (there is no tile n): 8 slots, with twice the VALU
+// each.  The reads of MFMAs 0 .. kDsAhead-1 open the iteration.  Groups are
+// filled in order, respecting dependences.  The softmax of a tile is ~115
+// VALU (32 fma, 32 exp, 32 add, 16 cvt_pk, bookkeeping), spread evenly.
 #ifndef FMHA_VALU_PER_SLOT
 #define FMHA_VALU_PER_SLOT 7
 #endif
@@ -171,20 +173,27 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 #endif
 constexpr int kValuPerSlot = FMHA_VALU_PER_SLOT;
 constexpr int kDsAhead = FMHA_DS_AHEAD;
-constexpr int ds_reads_of_mfma(int m) { return m < 8 ? 2 : (m < 16 ? 1 : 0); }
-constexpr int ds_reads_before(int n) { return n <= 0 ? 0 : ds_reads_of_mfma(n - 1) + ds_reads_before(n - 1); }
-template <int I>
-__device__ __forceinline__ void sched_slot() {
-    __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-    if constexpr (ds_reads_of_mfma(I + kDsAhead) > 0)
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, ds_reads_of_mfma(I + kDsAhead), 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedVALU, kValuPerSlot, 0);
-}
-template <int... Is>
-__device__ __forceinline__ void sched_iteration(std::integer_sequence<int, Is...>) {
-    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, ds_reads_before(kDsAhead), 0);
-    (sched_slot<Is>(), ...);
-}
+template <bool kG1, bool kG0>
+struct IterSchedule {
+    static constexpr int kMfma = 8 * (int(kG1) + int(kG0));
+    static constexpr int kValu = kMfma == 16 ? kValuPerSlot : 2 * kValuPerSlot;
+    static constexpr int reads(int m) { return m >= kMfma ? 0 : (kG1 && m < 8) ? 2 : 1; }
+    static constexpr int reads_before(int n) { return n <= 0 ? 0 : reads(n - 1) + reads_before(n - 1); }
+    template <int I>
+    static __device__ __forceinline__ void slot() {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        if constexpr (reads(I + kDsAhead) > 0) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, reads(I + kDsAhead), 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVALU, kValu, 0);
+    }
+    template <int... Is>
+    static __device__ __forceinline__ void run(std::integer_sequence<int, Is...>) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, reads_before(kDsAhead), 0);
+        (slot<Is>(), ...);
+    }
+    static __device__ __forceinline__ void apply() {
+        if constexpr (kMfma > 0) run(std::make_integer_sequence<int, kMfma>{});
+    }
+};
 
 // Online-softmax state of one lane's query row (both lane halves of a row keep
 // the same m_ref; l_part is this lane's partial sum).
@@ -363,7 +372,6 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const float scale = p.scale;          // log2(e)/sqrt(D)
     const float scale_v = in_vgpr(scale);  // the per-score fma's operand
     Softmax sm{kMaxSeed, 0.0f, 0.0f};
-    constexpr int kGroupSize = kWaves * 64;  // threads per key-range group
     f32x16 oacc[2];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
@@ -482,14 +490,16 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         }
         sm.l_part += sm.l_tile;
     };
-    auto interleave = [&]() { sched_iteration(std::make_integer_sequence<int, 16>{}); };
-
     f32x16 sacc[2][2];  // S^T of two consecutive tiles (alternating roles)
     bf16x8 pbuf[2][4];  // P^T of two consecutive tiles (alternating roles)
 
-    // iteration t (phase J = t % kRing): GEMM1(t-1) || GEMM0(t+1) || softmax(t)
-    auto iteration = [&](int t, auto phase_c) {
+    // iteration t (phase J = t % kRing): GEMM1(t-1) || GEMM0(t+1) || softmax(t).
+    // The first iteration has no GEMM1 (kG1 = false: there is no tile -1);
+    // every iteration waits, synchronises and refills the ring the same way,
+    // so all waves of a block pass the same barriers.
+    auto iteration = [&](int t, auto phase_c, auto g1_c, auto g0_c) {
         constexpr int J = decltype(phase_c)::value;
+        constexpr bool kG1 = decltype(g1_c)::value, kG0 = decltype(g0_c)::value;
         constexpr int cur = J & 1, nxt = cur ^ 1;
         // K(t+1) and V(t-1) were fetched three iterations ago; the loads of
         // the two previous iterations may still fly.
@@ -498,10 +508,10 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_k(t + kRing, std::integral_constant<int, J>{});
         issue_v(t + 2, std::integral_constant<int, (J + 2) % kRing>{});
         mask_tile(t, sacc[cur]);
-        gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[nxt]);
-        gemm0(std::integral_constant<int, (J + 1) % kRing>{}, sacc[nxt]);
+        if constexpr (kG1) gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[nxt]);
+        if constexpr (kG0) gemm0(std::integral_constant<int, (J + 1) % kRing>{}, sacc[nxt]);
         softmax(sacc[cur], pbuf[cur]);
-        interleave();
+        IterSchedule<kG1, kG0>::apply();
         settle(sacc[cur], pbuf[cur]);
     };
     // the last GEMM1, for tile t of phase J
@@ -515,22 +525,11 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;
     using P3 = std::integral_constant<int, 3>;
+    using Yes = std::true_type;
+    using No = std::false_type;
+    auto mid = [&](int t, auto phase_c) { iteration(t, phase_c, Yes{}, Yes{}); };
 
     if (ntg > 0) {
-        // GEMM1(-1) of iteration 0 runs on P = 0 and a zeroed V stage, which
-        // contributes exactly 0 and keeps the loop body branch-free.
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pbuf[1][i] = bf16x8{};
-        {
-            typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
-            // the threads sharing the stage region (a group, or the whole pair)
-            constexpr int kRegionThreads = kPair ? 2 * kGroupSize : kGroupSize;
-            static_assert(kTileBytes % (16 * kRegionThreads) == 0, "whole 16-byte stores per thread");
-            lds_i32x4* z = (lds_i32x4*)(ring.v[kRing - 1] + goff);
-            const int tir = kPair ? (int)threadIdx.x : (int)threadIdx.x % kGroupSize;
-#pragma unroll
-            for (int i = 0; i < kTileBytes / (16 * kRegionThreads); ++i) z[tir + i * kRegionThreads] = i32x4{};
-        }
         // prologue: K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once K0 landed
         issue_k(0, P0{});
         issue_k(1, P1{});
@@ -539,34 +538,38 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_v(1, P1{});
         issue_k(3, P3{});
         vmcnt_wait<5 * kLoads>();
-        ring_barrier();  // also completes the zeroing stores above (lgkmcnt)
+        ring_barrier();
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
         // speculative softmax holds from tile 0 on (rows with no visible key
         // there keep the finite seed: their P is exactly 0)
         mask_tile(0, sacc[0]);
         sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]));
-        int t = 0;
+        // iteration 0 has no GEMM1; iterations 1 .. ntg-1 run in groups of
+        // kRing (phases 1 2 3 0) and the 0-3 left over, each with GEMM0 of
+        // the next tile (for the last one a dead, zero-filled tile)
+        iteration(0, P0{}, No{}, Yes{});
+        int t = 1;
         for (; t + kRing <= ntg; t += kRing) {
-            iteration(t, P0{});
-            iteration(t + 1, P1{});
-            iteration(t + 2, P2{});
-            iteration(t + 3, P3{});
+            mid(t, P1{});
+            mid(t + 1, P2{});
+            mid(t + 2, P3{});
+            mid(t + 3, P0{});
         }
         const int rem = ntg - t;
         if (rem == 0) {
-            last_gemm1(P3{});
+            last_gemm1(P0{});
         } else {
-            iteration(t, P0{});
+            mid(t, P1{});
             if (rem == 1) {
-                last_gemm1(P0{});
+                last_gemm1(P1{});
             } else {
-                iteration(t + 1, P1{});
+                mid(t + 1, P2{});
                 if (rem == 2) {
-                    last_gemm1(P1{});
-                } else {
-                    iteration(t + 2, P2{});
                     last_gemm1(P2{});
+                } else {
+                    mid(t + 2, P3{});
+                    last_gemm1(P3{});
                 }
             }
         }
