@@ -105,7 +105,8 @@ def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
     """Launch on ``stream`` (a hipStream_t as int, or None for the null stream).
 
     ``variant``: VARIANT_AUTO (the launcher's choice), VARIANT_REGULAR (the
-    reference-named entries) or VARIANT_SPLITKV (the split-KV entries)."""
+    reference-named entries), VARIANT_SPLITKV (the split-KV entries) or
+    VARIANT_PAIR (the pair entries)."""
     lib = load_library()
     if variant == VARIANT_AUTO:
         rc = lib.fmha_fwd_d64_bf16(ctypes.byref(params), int(batch), int(causal), stream)

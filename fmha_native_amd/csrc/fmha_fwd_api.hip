@@ -17,6 +17,8 @@ namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+constexpr int kMaxGridYZ = 65535;  // largest grid y / z dimension
+
 // Largest byte offset touched inside one (batch, head) of a tensor with `rows`
 // rows must fit the 31-bit buffer offsets the kernel uses; the loaders may
 // read up to one 64-key tile past the last row (zero-filled by the bound).
@@ -50,6 +52,8 @@ extern "C" hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* p, int batch,
         return hipErrorInvalidValue;
     if (p->seqstart_q != nullptr && p->lse != nullptr && p->nhead_stride_q % p->stride_q != 0)
         return hipErrorInvalidValue;  // varlen LSE head stride is nhead_stride_q / stride_q
+    // grid (nhead_q, ceil(seqlen_q / kM0), batch): y and z are at most 65535
+    if ((p->seqlen_q + FMHA_KM0 - 1) / FMHA_KM0 > kMaxGridYZ || batch > kMaxGridYZ) return hipErrorInvalidValue;
     return hipSuccess;
 }
 

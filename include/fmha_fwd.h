@@ -40,7 +40,8 @@
  *  q,k,v,o non-NULL and 16-byte aligned; every stride a multiple of 8 elements
  *  (16-byte rows); seqlen_* >= 0; nhead_k > 0; nhead_q % nhead_k == 0; both or
  *  neither seqstart pointer set; every in-tensor offset of one (batch, head)
- *  fits in 31 bits.  Violations return hipErrorInvalidValue and launch nothing.
+ *  fits in 31 bits; the grid fits (ceil(seqlen_q / kM0) <= 65535 and
+ *  batch <= 65535).  Violations return hipErrorInvalidValue and launch nothing.
  */
 #ifndef FMHA_FWD_H_
 #define FMHA_FWD_H_

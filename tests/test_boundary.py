@@ -163,6 +163,8 @@ def _mut(**kw):
     (_mut(seqstart_q=0x15000), 1, 0),        # only one seqstart pointer
     (_mut(stride_k=1 << 23), 1, 0),          # offsets beyond 31 bits
     (_mut(varlen=True, nhead_stride_q=128 * 64 + 8), 1, 0),  # varlen LSE head stride not in rows
+    (_mut(seqlen_q=65535 * 128 + 1, lse=None), 1, 0),  # grid y = ceil(seqlen_q / 128) above 65535
+    (valid_params(), 65536, 0),                          # grid z = batch above 65535
     (valid_params(), -1, 0),
     (valid_params(), 1, 2),
 ])
