@@ -25,6 +25,7 @@ import numpy as np
 __all__ = [
     "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
     "tile_config", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
+    "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
     "VARIANTS",
 ]
@@ -35,6 +36,7 @@ LOG2E = 1.4426950408889634
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 HEAD_DIM = 64
+MERGE_MAX_PARTS = 64
 
 
 class FmhaError(RuntimeError):
@@ -85,6 +87,9 @@ def load_library(path=LIB_PATH):
     ip = ctypes.POINTER(ctypes.c_int)
     lib.fmha_fwd_d64_bf16_tile_config.argtypes = [ip, ip, ip, ip]
     lib.fmha_fwd_d64_bf16_tile_config.restype = None
+    i64, vp = ctypes.c_int64, ctypes.c_void_p
+    lib.fmha_merge_d64_bf16.argtypes = [ctypes.c_int, i64, vp, i64, vp, i64, i64, vp, vp, vp]
+    lib.fmha_merge_d64_bf16.restype = ctypes.c_int
     u16p = ctypes.POINTER(ctypes.c_uint16)
     lib.fmha_runner_fill_ref.argtypes = [ctypes.c_uint, u16p, ctypes.c_size_t, u16p, ctypes.c_size_t, u16p,
                                          ctypes.c_size_t]
@@ -206,4 +211,38 @@ def fmha_fwd(q, k, v, causal=False, return_lse=False, seqstart_q=None, seqstart_
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
     fmha_fwd_d64_bf16(p, batch, 1 if causal else 0, stream)
+    return o, lse
+
+
+def fmha_merge_d64_bf16(n_parts, rows, o_parts, o_part_stride, lse_parts, lse_part_stride, o_row_stride, o, lse,
+                        stream=None):
+    """The C-ABI merge of partial (O, LSE) results (device pointers as ints;
+    strides in elements).  Raises :class:`FmhaError` on a non-zero hipError_t."""
+    rc = load_library().fmha_merge_d64_bf16(int(n_parts), int(rows), o_parts, int(o_part_stride), lse_parts,
+                                            int(lse_part_stride), int(o_row_stride), o, lse, stream)
+    if rc != HIP_SUCCESS:
+        raise FmhaError(rc, "fmha_merge_d64_bf16")
+
+
+def merge_partials(o_parts, lse_parts, o=None, lse=None, stream=None):
+    """Merge partial results over disjoint key sets on torch device tensors.
+
+    ``o_parts``: bf16 [n, ..., 64] and ``lse_parts``: float32 [n, ...] with the
+    same ``...`` (rows in LSE order, e.g. [B, H, S] or [H, T]), both contiguous.
+    Returns (o, lse) with shapes [..., 64] and [...]; ``o``/``lse`` may be given.
+    """
+    import torch
+
+    n = o_parts.shape[0]
+    rows = lse_parts[0].numel()
+    if not (o_parts.is_contiguous() and lse_parts.is_contiguous()) or o_parts[0].numel() != rows * HEAD_DIM:
+        raise ValueError("o_parts [n, ..., 64] and lse_parts [n, ...] must be contiguous and agree")
+    if o is None:
+        o = torch.empty(o_parts.shape[1:], dtype=o_parts.dtype, device=o_parts.device)
+    if lse is None:
+        lse = torch.empty(lse_parts.shape[1:], dtype=torch.float32, device=lse_parts.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(o_parts.device).cuda_stream
+    fmha_merge_d64_bf16(n, rows, o_parts.data_ptr(), rows * HEAD_DIM, lse_parts.data_ptr(), rows, HEAD_DIM,
+                        o.data_ptr(), lse.data_ptr(), stream)
     return o, lse

@@ -118,7 +118,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
  *                         per two adjacent M-tiles of a (batch, head)
- * Both forms give the same results up to fp32 rounding order.  An unknown
+ * All forms give the same results up to fp32 rounding order.  An unknown
  * variant returns hipErrorInvalidValue. */
 #define FMHA_VARIANT_AUTO 0
 #define FMHA_VARIANT_REGULAR 1
@@ -134,6 +134,29 @@ hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int c
 /* Tile constants of the linked library, so FFI callers (ctypes, cgo) need not
  * parse this header: writes kM0, kN0, kBlockSize, head dim. */
 void fmha_fwd_d64_bf16_tile_config(int* m0, int* n0, int* block_size, int* head_dim);
+
+/* Merge of partial results over disjoint key sets (this build's own; no
+ * counterpart in the reference).  The LSE merge the split-KV form does in
+ * LDS, for partials from separate launches of fmha_fwd_d64_bf16 (key chunks of
+ * one sequence, ring attention, one GPU's shard of a sharded sequence).  For
+ * each row r with parts i = 0 .. n_parts-1 (O_i: 64 bf16, normalised; LSE_i:
+ * fp32 natural log, -inf for a part that saw no key):
+ *   LSE[r] = log(sum_i exp(LSE_i[r])),   O[r] = sum_i exp(LSE_i[r] - LSE[r]) O_i[r]
+ * and O = 0, LSE = -inf where every part is -inf (fp32 arithmetic, O rounded
+ * to nearest even bf16).  Rows are flattened in LSE order (dense BHSD
+ * [B][H][S], varlen [H][T]):
+ *   O_i row r at  o_parts + i*o_part_stride + r*o_row_stride   (bf16 elements)
+ *   LSE_i row r at lse_parts + i*lse_part_stride + r             (floats)
+ *   output row r at o + r*o_row_stride, lse + r (lse may be NULL)
+ * o_parts and o 16-byte aligned, strides multiples of 8 elements, o_row_stride
+ * >= 64, parts not overlapping, 1 <= n_parts <= FMHA_MERGE_MAX_PARTS; o may be
+ * part 0 itself (each output chunk is written after its last read).  Returns
+ * hipSuccess, hipErrorInvalidValue (nothing launched) or the launch error;
+ * allocates nothing. */
+#define FMHA_MERGE_MAX_PARTS 64
+hipError_t fmha_merge_d64_bf16(int n_parts, int64_t rows, const void* o_parts, int64_t o_part_stride,
+                               const float* lse_parts, int64_t lse_part_stride, int64_t o_row_stride, void* o,
+                               float* lse, hipStream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

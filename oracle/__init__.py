@@ -59,6 +59,9 @@ def load():
         lib.oracle_fill_ref.argtypes = [ctypes.c_uint, u16p, ctypes.c_size_t, u16p, ctypes.c_size_t, u16p,
                                         ctypes.c_size_t]
         lib.oracle_fill_ref.restype = None
+        i64, vp = ctypes.c_int64, ctypes.c_void_p
+        lib.oracle_merge_d64.argtypes = [ctypes.c_int, i64, vp, i64, vp, i64, i64, vp, vp]
+        lib.oracle_merge_d64.restype = None
         _lib = lib
     return _lib
 
@@ -132,3 +135,17 @@ def fill_ref(seed, nq, nk, nv):
     u16p = ctypes.POINTER(ctypes.c_uint16)
     load().oracle_fill_ref(seed, q.ctypes.data_as(u16p), nq, k.ctypes.data_as(u16p), nk, v.ctypes.data_as(u16p), nv)
     return q, k, v
+
+
+def merge(o_parts, lse_parts):
+    """float64 merge of partial results: ``o_parts`` uint16 bf16 bits [n, rows*64],
+    ``lse_parts`` float32 [n, rows].  Returns (O bits uint16 [rows*64], LSE [rows])."""
+    o_parts = np.ascontiguousarray(o_parts, dtype=np.uint16)
+    lse_parts = np.ascontiguousarray(lse_parts, dtype=np.float32)
+    n, rows = lse_parts.shape
+    assert o_parts.shape == (n, rows * 64)
+    o = np.empty(rows * 64, dtype=np.uint16)
+    lse = np.empty(rows, dtype=np.float32)
+    load().oracle_merge_d64(n, rows, o_parts.ctypes.data, rows * 64, lse_parts.ctypes.data, rows, 64, o.ctypes.data,
+                            lse.ctypes.data)
+    return o, lse

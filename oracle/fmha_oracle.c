@@ -31,6 +31,13 @@
  *    step 5's bf16 truncation of P (the one quantisation the reference adds to
  *    imitate its kernel).  Its difference to the faithful result is the
  *    oracle's own truncation error, used as an explicit allowance in tests.
+ *  - oracle_merge_d64(): the merge of partial results over disjoint key sets
+ *    (no reference counterpart; it checks this build's fmha_merge_d64_bf16):
+ *    LSE = log sum_i exp(LSE_i), O = sum_i exp(LSE_i - LSE) O_i in float64,
+ *    O rounded to nearest even bf16; O = 0, LSE = -inf when every part is -inf.
+ *    Pinned in tests/test_oracle.py by closed forms (one part is the identity,
+ *    equal LSEs average, -inf parts drop out) and by the identity that merging
+ *    the float64 attention of key chunks gives the attention of all keys.
  * Build with -ffp-contract=off so no multiply-add is fused (the reference's
  * host build has no FMA contraction either).
  */
@@ -368,4 +375,40 @@ void oracle_fill_ref(unsigned seed, uint16_t* q, size_t nq, uint16_t* k, size_t 
             float x = ((rand() % 1000) - 500) / 5000.0f;
             bufs[t][i] = f32_to_bf16_trunc(x);
         }
+}
+
+static inline uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* NaN stays NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+void oracle_merge_d64(int n_parts, int64_t rows, const uint16_t* o_parts, int64_t o_part_stride,
+                      const float* lse_parts, int64_t lse_part_stride, int64_t o_row_stride, uint16_t* o,
+                      float* lse) {
+    for (int64_t r = 0; r < rows; r++) {
+        double m = -INFINITY;
+        for (int i = 0; i < n_parts; i++) {
+            const double l = lse_parts[i * lse_part_stride + r];
+            if (l > m) m = l;
+        }
+        uint16_t* orow = o + r * o_row_stride;
+        if (m == -INFINITY) {
+            for (int d = 0; d < 64; d++) orow[d] = 0;
+            if (lse) lse[r] = -INFINITY;
+            continue;
+        }
+        double acc[64] = {0};
+        double w_sum = 0.0;
+        for (int i = 0; i < n_parts; i++) {
+            const double w = exp((double)lse_parts[i * lse_part_stride + r] - m);
+            const uint16_t* prow = o_parts + i * o_part_stride + r * o_row_stride;
+            w_sum += w;
+            for (int d = 0; d < 64; d++) acc[d] += w * (double)bf16_to_f32(prow[d]);
+        }
+        for (int d = 0; d < 64; d++) orow[d] = f32_to_bf16_rne((float)(acc[d] / w_sum));
+        if (lse) lse[r] = (float)(m + log(w_sum));
+    }
 }

@@ -46,6 +46,13 @@ int oracle_fmha_fwd_f64(const oracle_params* p, int batch, int causal, double* o
 /* The reference's srand/rand +-0.1 generator for Q, K, V in sequence. */
 void oracle_fill_ref(unsigned seed, uint16_t* q, size_t nq, uint16_t* k, size_t nk, uint16_t* v, size_t nv);
 
+/* Merge of partial results over disjoint key sets (the LSE merge; no
+ * reference counterpart), in float64, O rounded to nearest even bf16.
+ * Layout as the product's fmha_merge_d64_bf16 (strides in elements). */
+void oracle_merge_d64(int n_parts, int64_t rows, const uint16_t* o_parts, int64_t o_part_stride,
+                      const float* lse_parts, int64_t lse_part_stride, int64_t o_row_stride, uint16_t* o,
+                      float* lse);
+
 #ifdef __cplusplus
 }
 #endif

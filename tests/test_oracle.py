@@ -319,3 +319,96 @@ def test_rules():
     r = np.linspace(-1, 1, 128, dtype=np.float32)
     assert verify.reference_rule(r, r + 5e-4)["pass"]
     assert not verify.reference_rule(r, r + 2e-3)["pass"]
+
+
+# ---------------------------------------------------------------- partial-result merge
+
+def bf16_rne(x):
+    """float -> bf16 bits, round to nearest even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _random_parts(n, rows, seed):
+    rng = np.random.default_rng(seed)
+    o = bf16_rne(rng.standard_normal((n, rows * 64)))
+    lse = (rng.standard_normal((n, rows)) * 3).astype(np.float32)
+    return o, lse
+
+
+def test_merge_one_part_is_identity():
+    o, lse = _random_parts(1, 37, 1)
+    mo, ml = oracle.merge(o, lse)
+    assert np.array_equal(mo, o[0]) and np.array_equal(ml, lse[0])
+
+
+def test_merge_equal_lse_averages():
+    o, lse = _random_parts(3, 29, 2)
+    lse[:] = lse[0]
+    mo, ml = oracle.merge(o, lse)
+    mean = np.mean(verify.bf16_bits_to_f32(o).reshape(3, -1).astype(np.float64), axis=0)
+    assert np.array_equal(mo, bf16_rne(mean))
+    np.testing.assert_allclose(ml, lse[0] + np.log(3.0), rtol=1e-6, atol=1e-6)
+
+
+def test_merge_minus_inf_parts_drop_out():
+    o, lse = _random_parts(3, 41, 3)
+    lse[2, :] = -np.inf
+    lse[1, :5] = -np.inf
+    mo, ml = oracle.merge(o, lse)
+    mo2, ml2 = oracle.merge(o[:2], lse[:2])
+    assert np.array_equal(mo, mo2) and np.array_equal(ml, ml2)
+    lse[:, 7] = -np.inf  # every part empty for row 7: O = 0, LSE = -inf
+    mo, ml = oracle.merge(o, lse)
+    assert np.all(mo.reshape(41, 64)[7] == 0) and np.isneginf(ml[7])
+
+
+def _numpy_merge(o_parts, lse_parts, mistake=None):
+    o = verify.bf16_bits_to_f32(o_parts).reshape(lse_parts.shape + (64,)).astype(np.float64)
+    l = lse_parts.astype(np.float64)
+    m = l.max(axis=0)
+    w = np.exp(m - l) if mistake == "sign" else np.exp(l - m)
+    out = (w[..., None] * o).sum(axis=0)
+    if mistake != "no_renorm":
+        out /= w.sum(axis=0)[..., None]
+    return out.reshape(-1), m + np.log(w.sum(axis=0))
+
+
+def _chunked_f64(prob, q, k, v, cuts):
+    """float64 attention of each key chunk [c0, c1): (O bits bf16 RNE, LSE float32) per chunk."""
+    B, Hk, Sk = prob.batch, prob.nhead_k, prob.seqlen_k
+    k4, v4 = k.reshape(B, Hk, Sk, 64), v.reshape(B, Hk, Sk, 64)
+    o_parts, l_parts = [], []
+    for c0, c1 in zip(cuts[:-1], cuts[1:]):
+        pc = Problem(batch=B, nhead_q=prob.nhead_q, nhead_k=Hk, seqlen_q=prob.seqlen_q, seqlen_k=c1 - c0, lse=True)
+        oc, lc = oracle.run_f64(pc, q, np.ascontiguousarray(k4[:, :, c0:c1]).reshape(-1),
+                                np.ascontiguousarray(v4[:, :, c0:c1]).reshape(-1))
+        o_parts.append(bf16_rne(oc.astype(np.float32)))
+        l_parts.append(lc.astype(np.float32))
+    return np.stack(o_parts), np.stack(l_parts)
+
+
+def test_merge_of_key_chunks_is_full_attention():
+    """Merging the attention of disjoint key chunks gives the attention of all
+    keys (O within the bf16 rounding of the parts, LSE to float32); the merge
+    with a wrong exponent sign or without renormalisation does not."""
+    prob = Problem(batch=2, nhead_q=4, nhead_k=2, seqlen_q=37, seqlen_k=150, lse=True)
+    rng = np.random.default_rng(5)
+    nq, nk, _ = prob.sizes()
+    q, k, v = (bf16_rne(rng.standard_normal(n)) for n in (nq, nk, nk))
+    o_full, l_full = oracle.run_f64(prob, q, k, v)
+    o_parts, l_parts = _chunked_f64(prob, q, k, v, [0, 40, 41, 110, 150])
+    mo, ml = oracle.merge(o_parts, l_parts)
+    got = verify.bf16_bits_to_f32(mo).astype(np.float64)
+    # each part carries its own bf16 rounding (<= 2^-9 |O_i|), weighted by
+    # exp(LSE_i - LSE); the merged value adds one more rounding
+    w = np.exp(l_parts.astype(np.float64) - l_full[None, :])[..., None]
+    o_abs = np.abs(verify.bf16_bits_to_f32(o_parts).reshape(w.shape[:2] + (64,)).astype(np.float64))
+    tol = 2.0 ** -8 * ((w * o_abs).sum(axis=0).reshape(-1) + np.abs(o_full)) + 1e-7
+    assert np.all(np.abs(got - o_full) <= tol)
+    np.testing.assert_allclose(ml, l_full, rtol=0, atol=1e-5)
+    on, ln = _numpy_merge(o_parts, l_parts)
+    assert np.all(np.abs(on - o_full) <= tol)
+    for mistake in ("sign", "no_renorm"):
+        bad, _ = _numpy_merge(o_parts, l_parts, mistake)
+        assert not np.all(np.abs(bad - o_full) <= tol), mistake
