@@ -73,19 +73,34 @@ int device_cus() {
 }
 
 #ifndef FMHA_SPLIT_POLICY
-#define FMHA_SPLIT_POLICY 2  // 0: never split, 1: always, 2: by grid size
+#define FMHA_SPLIT_POLICY 2  // 0: always regular, 1: always split-KV, 2: by grid shape (pick_variant)
 #endif
 
-// The split-KV entries give each M-tile twice the waves (two 4-wave groups
-// per block, one block per CU), each walking half of its key range.  They pay
-// off when the regular grid (two resident blocks per CU) leaves compute units
-// short of work.  Measured on MI355X (256 CUs): +12-16% at 128-256 blocks,
-// +2% at 626, -4% at 1024.  The pair entries are never picked automatically
-// (within a few % of the regular entries either way).
-int pick_variant(int blocks) {
+// Form choice from the grid (measured on MI355X, 256 CUs, all forms on one
+// box; blocks = regular-grid blocks, pairs = pair-grid blocks):
+//  * split-KV (two 4-wave groups per M-tile, one block per CU, each group
+//    walking half of the keys): when the regular grid cannot fill the GPU —
+//    blocks <= CUs (+8-10% at 128-256 blocks), and for causal grids, whose
+//    heaviest M-tile is the critical path, below 1.5 blocks per CU (+16% at
+//    384) or up to 2 per CU with long M-tiles (seqlen_k >= 8192: +6% at 512).
+//    Elsewhere it loses 2-17% to the regular form.
+//  * pair (two adjacent M-tiles per 8-wave block, one block per CU): the two
+//    blocks a CU holds in the regular form progress unevenly, so each CU's
+//    last block runs alone; a pair block has no such tail, but pays a barrier
+//    across 8 waves.  It wins when the pair blocks fill whole rounds of the
+//    CUs and the M-tiles are long: +3-4% dense at seqlen_k >= 8192, +3-5%
+//    causal at >= 32768; with a partial last round it loses 8-17%.
+//  * regular: everything else (the dense B4 H16 S2048 and causal B1 H16 S8192
+//    benchmark grids among them).
+int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k) {
     if (FMHA_SPLIT_POLICY == 0) return FMHA_VARIANT_REGULAR;
     if (FMHA_SPLIT_POLICY == 1) return FMHA_VARIANT_SPLITKV;
-    return blocks < 3 * device_cus() ? FMHA_VARIANT_SPLITKV : FMHA_VARIANT_REGULAR;
+    const int cus = device_cus();
+    if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
+    if (causal && (2 * blocks < 3 * cus || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
+    const bool whole_rounds = pairs >= cus && pairs % cus == 0;
+    if (whole_rounds && seqlen_k >= (causal ? 32768 : 8192)) return FMHA_VARIANT_PAIR;
+    return FMHA_VARIANT_REGULAR;
 }
 
 }  // namespace
@@ -99,7 +114,9 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
     const bool varlen = p->seqstart_q != nullptr;
-    if (variant == FMHA_VARIANT_AUTO) variant = pick_variant(p->nhead_q * m_tiles * batch);
+    if (variant == FMHA_VARIANT_AUTO)
+        variant = pick_variant((int64_t)p->nhead_q * m_tiles * batch, (int64_t)p->nhead_q * ((m_tiles + 1) / 2) * batch,
+                               causal, p->seqlen_k);
     if (variant == FMHA_VARIANT_PAIR) {
         const dim3 pgrid(p->nhead_q, (m_tiles + 1) / 2, batch);
         const dim3 block(FMHA_SPLIT_KBLOCK);

@@ -104,8 +104,8 @@ typedef struct FmhaFwdParams {
  * Returns hipSuccess, hipErrorInvalidValue for rejected arguments (nothing is
  * launched), or the launch error.  Asynchronous like any kernel launch; it
  * allocates nothing (its only state is a per-device cache of the compute-unit
- * count), so concurrent calls are safe.  Grids with fewer than 3 blocks per
- * compute unit run the split-KV form (see fmha_fwd_d64_bf16_variant).
+ * count), so concurrent calls are safe.  The kernel form follows the grid
+ * (see fmha_fwd_d64_bf16_variant).
  * Replaces src/bench_fmha_fwd.cpp:174-191. */
 hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
                              hipStream_t stream);
@@ -113,7 +113,11 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 /* The same launch with the kernel form chosen by the caller (this build's
  * own; no counterpart in the reference):
  *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: split-KV when the
- *                         grid has fewer than 3 blocks per compute unit
+ *                         regular grid has at most one block per compute unit
+ *                         (causal: fewer than 1.5, or up to 2 with seqlen_k >= 8192);
+ *                         pair when its blocks fill whole rounds of the compute
+ *                         units and seqlen_k >= 8192 (causal: >= 32768); else
+ *                         the regular entries
  *   FMHA_VARIANT_REGULAR  the four reference-named entries (kBlockSize threads)
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
