@@ -21,7 +21,8 @@
 //    GEMM1(tile t-1) and GEMM0(tile t+1) interleaved with the softmax VALU
 //    work of tile t (sched_group_barrier): the three stages have no data
 //    dependence on each other inside an iteration, so one wave keeps the
-//    matrix core and the VALU busy at the same time.
+//    matrix core and the VALU busy at the same time.  The first iteration
+//    issues GEMM0(tile 1) only (there is no tile -1).
 //  * K and V tiles go HBM/L2 -> LDS directly (buffer_load_dwordx4 ... lds)
 //    in two 4-deep rings: K(t+4) and V(t+2) are fetched during iteration t,
 //    i.e. both three iterations before they are read; one s_barrier per tile.
