@@ -164,8 +164,12 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 // each).  The first iteration of a block has no GEMM1 (there is no tile -1)
 // and the last no GEMM0 (there is no tile n): 8 slots, with twice the VALU
 // each.  The reads of MFMAs 0 .. kDsAhead-1 open the iteration.  Groups are
-// filled in order, respecting dependences.  The softmax of a tile is ~115
-// VALU (32 fma, 32 exp, 32 add, 16 cvt_pk, bookkeeping), spread evenly.
+// filled in order, respecting dependences; VALU the groups do not claim is
+// placed by the scheduler, so the softmax of a tile (~115 VALU: 32 fma, 32
+// exp, 32 add, 16 cvt_pk, bookkeeping) lands as 8-11 per slot over the first
+// 12 slots and the last GEMM0 chain runs bare.  A rigid even spread (every
+// slot fenced with sched_barrier, 7 VALU each) gives the same bits and is
+// 2-3% slower on the benchmark grids.
 #ifndef FMHA_VALU_PER_SLOT
 #define FMHA_VALU_PER_SLOT 7
 #endif
