@@ -143,6 +143,8 @@ __device__ __forceinline__ float wave_sum_halves(float x) {
 
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
 
 __device__ __forceinline__ bf16x8 lds_read_b128(const lds_char* p) { return *(const lds_bf16x8*)p; }
 // 8 keys x 1 head-dim column of V for the GEMM1 A operand (two tr_b16 reads,
@@ -413,21 +415,17 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         const bool need = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
         if (need) {
             // element (kb, r) holds key key0 + 4h + c with c = 32kb + 8(r/4) + r%4;
-            // it is visible iff c <= d.  Bit c of the lane's 64-bit map says so;
-            // each element is then one bit extract + one bit-select.
+            // it is visible iff c <= d: one compare (c is an inline constant)
+            // and one select per element.
             const int lim = kCausal ? min(sk - 1, my_row + shift) : sk - 1;
             const int d = lim - (key0 + 4 * hi);
-            const uint32_t lo = d < 0 ? 0u : (d >= 31 ? 0xffffffffu : (2u << d) - 1u);
-            const uint32_t hi_bits = d < 32 ? 0u : (d >= 63 ? 0xffffffffu : (2u << (d - 32)) - 1u);
-            const uint32_t ninf = __float_as_uint(in_vgpr(-__builtin_inff()));
+            const float ninf = in_vgpr(-__builtin_inff());
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int c = 8 * (r >> 2) + (r & 3);
-                    const uint32_t bits = kb ? hi_bits : lo;
-                    const uint32_t m = (uint32_t)((int32_t)(bits << (31 - c)) >> 31);  // 0 or all ones
-                    s[kb][r] = __uint_as_float((__float_as_uint(s[kb][r]) & m) | (ninf & ~m));
+                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                    s[kb][r] = c <= d ? s[kb][r] : ninf;
                 }
         }
     };
@@ -619,7 +617,19 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const float l_tot = wave_sum_halves(sm.l_part);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     {
-        const int orow_off = my_row * p.stride_o * 2;
+        // O^T / l as bf16, transposed through 4 KiB of LDS private to the wave
+        // so that every store writes whole 128-byte rows (8 lanes per row, 8
+        // rows per instruction).  The K stages are idle here: their last reads
+        // and DMA writes completed before the last ring barrier (and with no
+        // tile at all none were issued).  Split-KV: the wave's own stage, whose
+        // hand-over data it has already read.  Lane (q, h) holds columns
+        // 32db + 8g4 + 4h .. +3 of row q, i.e. half of 16-byte chunk 4db + g4;
+        // chunk c of row q sits at c ^ (q & 7).
+        lds_char* const shared_stage =
+            wave_id < 2 ? ring.k[0] : wave_id < 4 ? ring.k[1] : wave_id < 6 ? ring.k[2] : ring.k[3];
+        lds_char* const own_stage = wave == 0 ? ring.k[0] : wave == 1 ? ring.k[1] : wave == 2 ? ring.k[2] : ring.k[3];
+        lds_char* const tb = kSplitKV ? own_stage : shared_stage + (wave_id & 1) * kRowsPerWave * kRowBytes;
+        static_assert(2 * kRowsPerWave * kRowBytes <= kTileBytes, "two waves' O tiles per K stage");
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -632,9 +642,18 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
                 i32x2 w;
                 w[0] = __builtin_bit_cast(int, a);
                 w[1] = __builtin_bit_cast(int, c);
-                const int d0 = 32 * db + 8 * g4 + 4 * hi;
-                __builtin_amdgcn_raw_buffer_store_b64(w, ro, orow_off + d0 * 2, 0, 0);
+                const int chunk = 4 * db + g4;
+                *(lds_i32x2*)(tb + l32 * kRowBytes + ((chunk ^ (l32 & 7)) << 4) + 8 * hi) = w;
             }
+        // other lanes' writes must land before the reads (LDS is in order per
+        // wave; the wait also keeps the compiler from reordering)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / 8; ++i) {
+            const int r = 8 * i + (lane >> 3), c = lane & 7;
+            const i32x4 v = *(const lds_i32x4*)(tb + r * kRowBytes + ((c ^ (r & 7)) << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * p.stride_o * 2 + c * 16, 0, 0);
+        }
     }
     if (p.lse != nullptr && hi == 0 && my_row < sq) {
         float* lse_base;
