@@ -307,10 +307,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
             qop[t] = __builtin_bit_cast(bf16x8, raw);
         }
-        // Retire the Q loads here, visibly to the compiler: otherwise it keeps
-        // them "pending" into the loop and waits vmcnt there, which would also
-        // wait for the in-flight K/V prefetch.
-        asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
+        // retired in the prologue, after the first K tile's wait (below)
     }
 
     // ---- global -> LDS tile loaders: per tile each wave moves kLoads x 1 KiB
@@ -540,8 +537,14 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         issue_k(2, P2{});
         issue_v(1, P1{});
         issue_k(3, P3{});
-        vmcnt_wait<5 * kLoads>();
+        vmcnt_wait<5 * kLoads>();  // the Q loads (issued first) and K0 have landed
         ring_barrier();
+        // Retire the Q loads here, visibly to the compiler: its own wait then
+        // falls where the one above already holds (Q and K0 arrive in one
+        // memory latency, not two in a row), and it does not keep them
+        // pending into the loop, where its wait would also cover the K/V
+        // prefetch in flight.
+        asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
         // speculative softmax holds from tile 0 on (rows with no visible key
