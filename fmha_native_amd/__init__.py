@@ -24,7 +24,7 @@ import numpy as np
 
 __all__ = [
     "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
-    "tile_config", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
+    "tile_config", "pick_variant", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
     "VARIANTS",
@@ -84,6 +84,8 @@ def load_library(path=LIB_PATH):
     lib.fmha_fwd_d64_bf16_variant.restype = ctypes.c_int
     lib.fmha_fwd_d64_bf16_check.argtypes = [P, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_check.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_pick_variant.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.fmha_fwd_d64_bf16_pick_variant.restype = ctypes.c_int
     ip = ctypes.POINTER(ctypes.c_int)
     lib.fmha_fwd_d64_bf16_tile_config.argtypes = [ip, ip, ip, ip]
     lib.fmha_fwd_d64_bf16_tile_config.restype = None
@@ -124,6 +126,13 @@ def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
 def check_params(params, batch, causal):
     """Host-only argument check; returns the hipError_t code (0 = accepted)."""
     return load_library().fmha_fwd_d64_bf16_check(ctypes.byref(params), int(batch), int(causal))
+
+
+def pick_variant(params, batch, causal, compute_units=0):
+    """The form VARIANT_AUTO resolves to on a device with ``compute_units``
+    CUs (0 = the current device's); -1 for rejected arguments.  Host only."""
+    return load_library().fmha_fwd_d64_bf16_pick_variant(ctypes.byref(params), int(batch), int(causal),
+                                                          int(compute_units))
 
 
 def tile_config():

@@ -82,8 +82,8 @@ int device_cus() {
 //    walking half of the keys): when the regular grid cannot fill the GPU —
 //    blocks <= CUs (+8-10% at 128-256 blocks), and for causal grids, whose
 //    heaviest M-tile is the critical path, below 1.5 blocks per CU (+16% at
-//    384) or up to 2 per CU with long M-tiles (seqlen_k >= 8192: +6% at 512).
-//    Elsewhere it loses 2-17% to the regular form.
+//    384 = 1.5 per CU) or up to 2 per CU with long M-tiles (seqlen_k >= 8192:
+//    +6% at 512).  Elsewhere it loses 2-17% to the regular form.
 //  * pair (two adjacent M-tiles per 8-wave block, one block per CU): the two
 //    blocks a CU holds in the regular form progress unevenly, so each CU's
 //    last block runs alone; a pair block has no such tail, but pays a barrier
@@ -92,18 +92,31 @@ int device_cus() {
 //    causal at >= 32768; with a partial last round it loses 8-17%.
 //  * regular: everything else (the dense B4 H16 S2048 and causal B1 H16 S8192
 //    benchmark grids among them).
-int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k) {
+int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int cus) {
     if (FMHA_SPLIT_POLICY == 0) return FMHA_VARIANT_REGULAR;
     if (FMHA_SPLIT_POLICY == 1) return FMHA_VARIANT_SPLITKV;
-    const int cus = device_cus();
     if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
-    if (causal && (2 * blocks < 3 * cus || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
+    if (causal && (2 * blocks <= 3 * cus || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
     const bool whole_rounds = pairs >= cus && pairs % cus == 0;
     if (whole_rounds && seqlen_k >= (causal ? 32768 : 8192)) return FMHA_VARIANT_PAIR;
     return FMHA_VARIANT_REGULAR;
 }
 
+// blocks of the regular grid and of the pair grid
+int64_t grid_blocks(const FmhaFwdParams* p, int batch) {
+    return (int64_t)p->nhead_q * ((p->seqlen_q + kM0 - 1) / kM0) * batch;
+}
+int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
+    return (int64_t)p->nhead_q * (((p->seqlen_q + kM0 - 1) / kM0 + 1) / 2) * batch;
+}
+
 }  // namespace
+
+extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch, int causal, int compute_units) {
+    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
+    return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k,
+                        compute_units > 0 ? compute_units : device_cus());
+}
 
 extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batch, int causal, int variant,
                                                 hipStream_t stream) {
@@ -115,8 +128,7 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     const dim3 grid(p->nhead_q, m_tiles, batch);
     const bool varlen = p->seqstart_q != nullptr;
     if (variant == FMHA_VARIANT_AUTO)
-        variant = pick_variant((int64_t)p->nhead_q * m_tiles * batch, (int64_t)p->nhead_q * ((m_tiles + 1) / 2) * batch,
-                               causal, p->seqlen_k);
+        variant = pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus());
     if (variant == FMHA_VARIANT_PAIR) {
         const dim3 pgrid(p->nhead_q, (m_tiles + 1) / 2, batch);
         const dim3 block(FMHA_SPLIT_KBLOCK);

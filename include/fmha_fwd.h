@@ -114,7 +114,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  * own; no counterpart in the reference):
  *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: split-KV when the
  *                         regular grid has at most one block per compute unit
- *                         (causal: fewer than 1.5, or up to 2 with seqlen_k >= 8192);
+ *                         (causal: at most 1.5, or up to 2 with seqlen_k >= 8192);
  *                         pair when its blocks fill whole rounds of the compute
  *                         units and seqlen_k >= 8192 (causal: >= 32768); else
  *                         the regular entries
@@ -134,6 +134,12 @@ hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int
 /* Argument checks of fmha_fwd_d64_bf16 without launching (host only, no GPU
  * needed).  Returns hipSuccess or hipErrorInvalidValue. */
 hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int causal);
+
+/* The form FMHA_VARIANT_AUTO resolves to for these arguments on a device with
+ * `compute_units` compute units (0 = the current device's count), without
+ * launching (this build's own; no counterpart in the reference).  Returns
+ * FMHA_VARIANT_REGULAR, _SPLITKV or _PAIR, or -1 for rejected arguments. */
+int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* params, int batch, int causal, int compute_units);
 
 /* Tile constants of the linked library, so FFI callers (ctypes, cgo) need not
  * parse this header: writes kM0, kN0, kBlockSize, head dim. */

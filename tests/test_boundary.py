@@ -187,6 +187,48 @@ def test_null_params_pointer():
     assert lib.fmha_fwd_d64_bf16_check(None, 1, 0) == INVALID
 
 
+# ---------------------------------------------------------------- kernel-form policy
+
+def _shape(batch, heads, seqlen):
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = heads
+    p.seqlen_q = p.seqlen_k = seqlen
+    return p, batch
+
+
+R, S, P = fmha.VARIANT_REGULAR, fmha.VARIANT_SPLITKV, fmha.VARIANT_PAIR
+
+
+@pytest.mark.parametrize("batch,heads,seqlen,causal,cus,form", [
+    (1, 8, 4096, 0, 256, S),     # 256 blocks: at most one per CU
+    (1, 12, 4096, 0, 256, R),    # 384 dense blocks
+    (1, 12, 4096, 1, 256, S),    # 384 causal blocks = 1.5 per CU: still split
+    (1, 13, 4096, 1, 256, R),    # 416 causal blocks, short M-tiles
+    (1, 8, 8192, 1, 256, S),     # 512 causal blocks with seqlen_k >= 8192
+    (1, 32, 2048, 1, 256, R),    # 512 causal blocks, short M-tiles
+    (4, 16, 2048, 0, 256, R),    # cfg2
+    (1, 16, 8192, 1, 256, R),    # cfg3: whole pair rounds but seqlen_k < 32768
+    (1, 8, 8192, 0, 256, P),     # 256 pair blocks, long M-tiles
+    (1, 4, 32768, 1, 256, P),    # 512 causal pair blocks, seqlen_k >= 32768
+    (1, 2, 40000, 0, 256, R),    # 314 pair blocks: a partial last round
+    (1, 2, 40000, 1, 256, R),    # cfg5
+    (1, 8, 4096, 0, 304, S),     # the rule scales with the CU count
+    (4, 16, 2048, 0, 304, R),
+    (1, 19, 8192, 0, 304, P),    # 19 * 32 = 608 pair blocks = 2 rounds of 304
+])
+def test_auto_form_rule(batch, heads, seqlen, causal, cus, form):
+    """The launcher's documented rule (grid shape -> kernel form), host only."""
+    p, b = _shape(batch, heads, seqlen)
+    assert fmha.pick_variant(p, b, causal, cus) == form
+
+
+def test_auto_form_rejects_what_the_launch_rejects():
+    assert fmha.pick_variant(_mut(q=None), 1, 0, 256) == -1
+    assert fmha.pick_variant(valid_params(), 1, 2, 256) == -1
+    assert fmha.pick_variant(valid_params(), 1, 0, -1) == -1
+    assert fmha.pick_variant(valid_params(), 1, 0) in (R, S, P)  # the current device's count
+
+
 # ---------------------------------------------------------------- bench contract
 
 def test_bench_refuses_more_than_one_gpu():
