@@ -625,36 +625,44 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         // rows per instruction).  The K stages are idle here: their last reads
         // and DMA writes completed before the last ring barrier (and with no
         // tile at all none were issued).  Split-KV: the wave's own stage, whose
-        // hand-over data it has already read.  Lane (q, h) holds columns
-        // 32db + 8g4 + 4h .. +3 of row q, i.e. half of 16-byte chunk 4db + g4;
-        // chunk c of row q sits at c ^ (q & 7).
+        // hand-over data it has already read.
         lds_char* const shared_stage =
             wave_id < 2 ? ring.k[0] : wave_id < 4 ? ring.k[1] : wave_id < 6 ? ring.k[2] : ring.k[3];
         lds_char* const own_stage = wave == 0 ? ring.k[0] : wave == 1 ? ring.k[1] : wave == 2 ? ring.k[2] : ring.k[3];
         lds_char* const tb = kSplitKV ? own_stage : shared_stage + (wave_id & 1) * kRowsPerWave * kRowBytes;
         static_assert(2 * kRowsPerWave * kRowBytes <= kTileBytes, "two waves' O tiles per K stage");
+        // Lane (q, h) holds columns 8c + 4h .. +3 of row q, half h of 16-byte
+        // chunk c = 4db + g4.  In the buffer, chunk c of row q sits at chunk
+        // c ^ ((q >> 1) & 7), and odd rows swap the two 8-byte halves.  LDS
+        // takes a 64-lane 8-byte write 16 lanes (128 bytes) at a time: each
+        // such group (rows of both parities, so both halves) writes 128
+        // distinct bank positions.  The reads take whole rows, 16 bytes a lane
+        // (2 rows = 256 bytes per group), conflict free in any order; odd rows
+        // swap their halves back in registers.
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-                bf16x2 a, c;
+                bf16x2 a, b;
                 a[0] = (__bf16)(oacc[db][4 * g4 + 0] * inv);
                 a[1] = (__bf16)(oacc[db][4 * g4 + 1] * inv);
-                c[0] = (__bf16)(oacc[db][4 * g4 + 2] * inv);
-                c[1] = (__bf16)(oacc[db][4 * g4 + 3] * inv);
+                b[0] = (__bf16)(oacc[db][4 * g4 + 2] * inv);
+                b[1] = (__bf16)(oacc[db][4 * g4 + 3] * inv);
                 i32x2 w;
                 w[0] = __builtin_bit_cast(int, a);
-                w[1] = __builtin_bit_cast(int, c);
-                const int chunk = 4 * db + g4;
-                *(lds_i32x2*)(tb + l32 * kRowBytes + ((chunk ^ (l32 & 7)) << 4) + 8 * hi) = w;
+                w[1] = __builtin_bit_cast(int, b);
+                const int c = 4 * db + g4;
+                *(lds_i32x2*)(tb + l32 * kRowBytes + ((c ^ ((l32 >> 1) & 7)) << 4) + 8 * (hi ^ (l32 & 1))) = w;
             }
         // other lanes' writes must land before the reads (LDS is in order per
         // wave; the wait also keeps the compiler from reordering)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < kRowsPerWave / 8; ++i) {
-            const int r = 8 * i + (lane >> 3), c = lane & 7;
-            const i32x4 v = *(const lds_i32x4*)(tb + r * kRowBytes + ((c ^ (r & 7)) << 4));
+            const int r = 8 * i + (lane >> 3), pc = lane & 7;  // physical chunk pc holds chunk pc ^ ((r >> 1) & 7)
+            const i32x4 raw = *(const lds_i32x4*)(tb + r * kRowBytes + (pc << 4));
+            const i32x4 v = (r & 1) ? i32x4{raw[2], raw[3], raw[0], raw[1]} : raw;  // odd rows: halves back in order
+            const int c = pc ^ ((r >> 1) & 7);
             __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * p.stride_o * 2 + c * 16, 0, 0);
         }
     }

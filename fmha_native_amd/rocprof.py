@@ -165,7 +165,8 @@ def main():
         rows.append((wl, k, c, ghz, mfma_busy, iters))
     md += ["| | " + " | ".join(r[0] for r in rows) + " |", "|---|" + "---|" * len(rows)]
     md.append("| kernel | " + " | ".join(f"`{r[1]}`" for r in rows) + " |")
-    md.append("| VGPR / AGPR / SGPR | " + " | ".join(f"{r[2]['vgpr']} / {r[2]['agpr']} / {r[2]['sgpr']}" for r in rows) + " |")
+    md.append("| VGPR / AGPR / SGPR (rocprofv3 dispatch fields) | "
+              + " | ".join(f"{r[2]['vgpr']} / {r[2]['agpr']} / {r[2]['sgpr']}" for r in rows) + " |")
     md.append("| LDS bytes per block | " + " | ".join(f"{r[2]['lds_bytes']}" for r in rows) + " |")
     md.append("| clock from GRBM_GUI_ACTIVE / 8 XCDs | " + " | ".join(f"{r[3]:.2f} GHz" for r in rows) + " |")
     md.append("| MFMA busy (per SIMD, of kernel cycles) | " + " | ".join(f"{100 * r[4]:.1f}%" for r in rows) + " |")
@@ -174,7 +175,11 @@ def main():
     md.append("| VALU instr per wave per 64-key tile (incl. 16 MFMA) | "
               + " | ".join(f"{r[2]['SQ_INSTS_VALU'] / r[5]:.1f}" for r in rows) + " |")
     md.append("| LDS instr per wave per tile | " + " | ".join(f"{r[2]['SQ_INSTS_LDS'] / r[5]:.1f}" for r in rows) + " |")
-    md += ["", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
+    md += ["", "The compiler reports 248-254 VGPRs used per wave for these entries (`; NumVgprs`, checked with "
+           "`tests/test_codegen.py`), allocated as 256: two waves per SIMD. rocprofv3's VGPR field is consistent "
+           "with the descriptor's granule count read as 4 registers per granule where gfx950 wave64 allocates "
+           "8 (31 + 1 granules: 128 shown, 256 allocated).",
+           "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
 
     path = args.summary or os.path.join(args.out, "summary.md")
     with open(path, "w") as f:
