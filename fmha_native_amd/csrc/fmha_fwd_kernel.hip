@@ -298,17 +298,9 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int wrow0 = row0 + wave * kRowsPerWave;  // first query row of this wave
     const int my_row = wrow0 + l32;                // this lane's query row
 
-    // ---- Q^T operand (B of GEMM0): lane (q, h) holds Q[q][16t + 8h .. +7] ----
+    // ---- Q^T operand (B of GEMM0): lane (q, h) holds Q[q][16t + 8h .. +7];
+    // loaded first thing in the prologue (a block with no key tile skips it) ----
     bf16x8 qop[4];
-    {
-        const int qoff = my_row * p.stride_q * 2 + hi * 16;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
-            qop[t] = __builtin_bit_cast(bf16x8, raw);
-        }
-        // retired in the prologue, after the first K tile's wait (below)
-    }
 
     // ---- global -> LDS tile loaders: per tile each wave moves kLoads x 1 KiB
     // of K (or V).  Lane L of load i writes LDS row 8*(kLoads*w+i) + L/8
@@ -530,7 +522,16 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     auto mid = [&](int t, auto phase_c) { iteration(t, phase_c, Yes{}, Yes{}); };
 
     if (ntg > 0) {
-        // prologue: K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once K0 landed
+        // prologue: Q, then K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once
+        // Q and K0 landed
+        {
+            const int qoff = my_row * p.stride_q * 2 + hi * 16;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
+                qop[t] = __builtin_bit_cast(bf16x8, raw);
+            }
+        }
         issue_k(0, P0{});
         issue_k(1, P1{});
         issue_v(0, P0{});
