@@ -121,6 +121,25 @@ def test_varlen_equals_per_sequence_dense_bitwise(form):
 
 
 @pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("seqlen,heads", [(700, 8), (11000, 8)])
+def test_causal_batch_equals_single_batches_bitwise(form, seqlen, heads):
+    """A causal grid with several batches (heaviest M-tiles first within each
+    batch) gives each batch the bits of a batch-1 launch of its own, for short
+    and long sequences (3 x 700 and 3 x 11,000 keys)."""
+    b = 3
+    pb = Problem(batch=b, nhead_q=heads, seqlen_q=seqlen, causal=True, lse=True)
+    q, k, v = make_inputs(pb, "normal", 21)
+    ob, lb = run_kernel(pb, q, k, v, variant=FORMS[form])
+    per = heads * seqlen
+    for i in range(b):
+        p1 = Problem(batch=1, nhead_q=heads, seqlen_q=seqlen, causal=True, lse=True)
+        o1, l1 = run_kernel(p1, q[i * per * 64:(i + 1) * per * 64], k[i * per * 64:(i + 1) * per * 64],
+                            v[i * per * 64:(i + 1) * per * 64], variant=FORMS[form])
+        assert np.array_equal(o1, ob[i * per * 64:(i + 1) * per * 64]), i
+        assert np.array_equal(l1, lb[i * per:(i + 1) * per]), i
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 def test_masked_and_foreign_keys_contribute_nothing(form):
     """Keys a row must not see are poisoned (K = 0, so the score is 0 and a
     wrongly included key would get a sizeable weight; V = 16384.0); the
