@@ -168,6 +168,43 @@ def varlen_lengths(seed, n, lo, hi):
     return list(out)
 
 
+def _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q):
+    import torch
+
+    varlen = seqstart_q is not None
+    rank = 3 if varlen else 4
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        if t.dim() != rank:
+            raise ValueError(f"{name} must have {rank} dimensions ({'[H, T, 64]' if varlen else '[B, H, S, 64]'} "
+                             f"view), got {tuple(t.shape)}")
+        if t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+            raise ValueError(f"{name} needs a contiguous last dimension of {HEAD_DIM}")
+    if tuple(o.shape) != tuple(q.shape):
+        raise ValueError(f"o {tuple(o.shape)} must have q's shape {tuple(q.shape)}")
+    if tuple(k.shape) != tuple(v.shape):
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must have the same shape")
+    if varlen:
+        if seqstart_k is None or max_seqlen_q is None:
+            raise ValueError("varlen needs seqstart_q, seqstart_k and max_seqlen_q")
+        for name, t in (("seqstart_q", seqstart_q), ("seqstart_k", seqstart_k)):
+            if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous 1-D int32 tensor")
+        if seqstart_q.numel() != seqstart_k.numel() or seqstart_q.numel() < 1:
+            raise ValueError("seqstart_q and seqstart_k need the same batch + 1 entries")
+    elif seqstart_k is not None:
+        raise ValueError("seqstart_k without seqstart_q")
+    elif q.shape[0] != k.shape[0]:
+        raise ValueError(f"q and k batch sizes differ ({q.shape[0]} vs {k.shape[0]})")
+    if lse is not None:
+        if lse.dtype != torch.float32 or tuple(lse.shape) != tuple(q.shape[:-1]) or not lse.is_contiguous():
+            raise ValueError(f"lse must be a contiguous float32 tensor of shape {tuple(q.shape[:-1])}")
+    tensors = [q, k, v, o] + [t for t in (lse, seqstart_q, seqstart_k) if t is not None]
+    if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
+        raise ValueError("all tensors must be on the same GPU")
+
+
 def params_from_tensors(q, k, v, o, lse=None, seqstart_q=None, seqstart_k=None, max_seqlen_q=None,
                         max_seqlen_k=None, scale=None):
     """Build FmhaFwdParams from device tensors.
@@ -176,7 +213,10 @@ def params_from_tensors(q, k, v, o, lse=None, seqstart_q=None, seqstart_k=None, 
     strides (BHSD, or BSHD permuted to that order).  Varlen: q/o are
     [Hq, T, 64], k/v [Hk, T, 64], with int32 ``seqstart_*`` of batch+1 entries.
     ``lse``: float32, [B, Hq, Sq] (dense) or [Hq, T] (varlen), contiguous.
+    Raises ValueError for tensors the kernel cannot take (dtype, rank, head
+    dim, inner stride, mismatched shapes, or memory that is not on one GPU).
     """
+    _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q)
     p = FmhaFwdParams()
     p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     p.lse = lse.data_ptr() if lse is not None else None

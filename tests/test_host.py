@@ -132,3 +132,57 @@ def test_sweep_protocol_and_table(tmp_path, capsys):
     sweep.main(["--bench", str(bad)])
     out = capsys.readouterr().out
     assert "ERROR" in out and "HIP error 98" in out
+
+
+# ---------------------------------------------------------------- torch tensor checks
+
+def _bf16(*shape):
+    import torch
+
+    return torch.zeros(shape, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("case,match", [
+    ("dtype", "bfloat16"),
+    ("rank", "dimensions"),
+    ("head_dim", "last dimension of 64"),
+    ("inner_stride", "last dimension of 64"),
+    ("o_shape", "q's shape"),
+    ("kv_shape", "same shape"),
+    ("batch", "batch sizes differ"),
+    ("lse", "lse must be"),
+    ("seqstart_dtype", "int32"),
+    ("seqstart_k_only", "seqstart_k without"),
+    ("cpu", "same GPU"),
+])
+def test_params_from_tensors_rejects(case, match):
+    """Tensors the kernel cannot take are refused before any pointer is used
+    (a host tensor's address would be read by the GPU)."""
+    import torch
+
+    q, k, v, o = _bf16(2, 4, 100, 64), _bf16(2, 2, 120, 64), _bf16(2, 2, 120, 64), _bf16(2, 4, 100, 64)
+    kw = {}
+    if case == "dtype":
+        q = q.float()
+    elif case == "rank":
+        q, o = q[0], o[0]
+    elif case == "head_dim":
+        q, o = _bf16(2, 4, 100, 32), _bf16(2, 4, 100, 32)
+    elif case == "inner_stride":
+        q = _bf16(2, 4, 100, 128)[..., ::2]
+    elif case == "o_shape":
+        o = _bf16(2, 4, 99, 64)
+    elif case == "kv_shape":
+        v = _bf16(2, 2, 121, 64)
+    elif case == "batch":
+        k, v = _bf16(3, 2, 120, 64), _bf16(3, 2, 120, 64)
+    elif case == "lse":
+        kw["lse"] = torch.zeros((2, 4, 99), dtype=torch.float32)
+    elif case == "seqstart_dtype":
+        q, k, v, o = _bf16(4, 300, 64), _bf16(2, 300, 64), _bf16(2, 300, 64), _bf16(4, 300, 64)
+        ss = torch.tensor([0, 100, 300], dtype=torch.int64)
+        kw.update(seqstart_q=ss, seqstart_k=ss, max_seqlen_q=200)
+    elif case == "seqstart_k_only":
+        kw["seqstart_k"] = torch.tensor([0, 100], dtype=torch.int32)
+    with pytest.raises(ValueError, match=match):
+        fmha.params_from_tensors(q, k, v, o, **kw)
