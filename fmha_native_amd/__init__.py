@@ -24,10 +24,10 @@ import numpy as np
 
 __all__ = [
     "FmhaError", "FmhaFwdParams", "LIB_PATH", "load_library", "fmha_fwd_d64_bf16", "check_params",
-    "tile_config", "pick_variant", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
+    "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANTS",
+    "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -86,6 +86,8 @@ def load_library(path=LIB_PATH):
     lib.fmha_fwd_d64_bf16_check.restype = ctypes.c_int
     lib.fmha_fwd_d64_bf16_pick_variant.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_pick_variant.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_tile_major.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    lib.fmha_fwd_d64_bf16_tile_major.restype = ctypes.c_int
     ip = ctypes.POINTER(ctypes.c_int)
     lib.fmha_fwd_d64_bf16_tile_config.argtypes = [ip, ip, ip, ip]
     lib.fmha_fwd_d64_bf16_tile_config.restype = None
@@ -105,6 +107,9 @@ def load_library(path=LIB_PATH):
 
 
 VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR = 0, 1, 2, 3
+# flag OR-ed into a variant: causal dense batches run batch after batch on the
+# reference's grid, never on the tile-major entries (results are identical)
+VARIANT_REFERENCE_ORDER = 16
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR}
 
 
@@ -113,7 +118,9 @@ def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
 
     ``variant``: VARIANT_AUTO (the launcher's choice), VARIANT_REGULAR (the
     reference-named entries), VARIANT_SPLITKV (the split-KV entries) or
-    VARIANT_PAIR (the pair entries)."""
+    VARIANT_PAIR (the pair entries), each optionally OR-ed with
+    VARIANT_REFERENCE_ORDER (keep the reference's batch-after-batch block order
+    for causal dense batches)."""
     lib = load_library()
     if variant == VARIANT_AUTO:
         rc = lib.fmha_fwd_d64_bf16(ctypes.byref(params), int(batch), int(causal), stream)
@@ -133,6 +140,13 @@ def pick_variant(params, batch, causal, compute_units=0):
     CUs (0 = the current device's); -1 for rejected arguments.  Host only."""
     return load_library().fmha_fwd_d64_bf16_pick_variant(ctypes.byref(params), int(batch), int(causal),
                                                           int(compute_units))
+
+
+def tile_major(params, batch, causal):
+    """1 when the launch runs a tile-major causal entry (every batch's heaviest
+    M-tiles first), 0 for the reference's batch-after-batch order, -1 for
+    rejected arguments.  Host only."""
+    return load_library().fmha_fwd_d64_bf16_tile_major(ctypes.byref(params), int(batch), int(causal))
 
 
 def tile_config():

@@ -11,6 +11,7 @@
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
 //   --variant auto|regular|splitkv|pair   kernel form (default: the launcher's choice)
+//   --order auto|reference   causal block order (reference: batch after batch)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
 
@@ -43,6 +44,7 @@ struct Config {
     unsigned seed = 42;
     std::string dist = "ref";
     int variant = FMHA_VARIANT_AUTO;
+    bool reference_order = false;
     float scale_inputs = 1.0f;
     std::vector<int> varlen_seqs;
 };
@@ -63,7 +65,8 @@ static void usage(const char* prog) {
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
-           "  --variant V      auto|regular|splitkv|pair kernel form [auto]\n",
+           "  --variant V      auto|regular|splitkv|pair kernel form [auto]\n"
+           "  --order O        auto|reference causal block order [auto]\n",
            prog);
 }
 
@@ -84,6 +87,7 @@ static Config parse(int argc, char** argv) {
                                    {"dist", required_argument, 0, 4},
                                    {"scale-inputs", required_argument, 0, 5},
                                    {"variant", required_argument, 0, 7},
+                                   {"order", required_argument, 0, 8},
                                    {"help", no_argument, 0, 0},
                                    {0, 0, 0, 0}};
     int ch, idx;
@@ -117,6 +121,11 @@ static Config parse(int argc, char** argv) {
                 else if (!strcmp(optarg, "splitkv")) c.variant = FMHA_VARIANT_SPLITKV;
                 else if (!strcmp(optarg, "pair")) c.variant = FMHA_VARIANT_PAIR;
                 else { fprintf(stderr, "Error: --variant must be auto, regular, splitkv or pair\n"); exit(1); }
+                break;
+            case 8:
+                if (!strcmp(optarg, "auto")) c.reference_order = false;
+                else if (!strcmp(optarg, "reference")) c.reference_order = true;
+                else { fprintf(stderr, "Error: --order must be auto or reference\n"); exit(1); }
                 break;
             case 0: usage(argv[0]); exit(0);
             default: usage(argv[0]); exit(1);
@@ -206,7 +215,9 @@ int main(int argc, char** argv) {
     }
 
     auto launch = [&]() {
-        hipError_t e = fmha_fwd_d64_bf16_variant(&p, c.batch, c.mask, c.variant, nullptr);
+        hipError_t e = fmha_fwd_d64_bf16_variant(&p, c.batch, c.mask,
+                                                c.variant | (c.reference_order ? FMHA_VARIANT_REFERENCE_ORDER : 0),
+                                                nullptr);
         if (e != hipSuccess) {
             fprintf(stderr, "fmha_fwd_d64_bf16 failed: %d (%s)\n", (int)e, hipGetErrorString(e));
             exit(1);

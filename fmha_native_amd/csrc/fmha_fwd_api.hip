@@ -102,6 +102,21 @@ int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int cu
     return FMHA_VARIANT_REGULAR;
 }
 
+// Causal dense grids of more than one batch run on the tile-major entries
+// (grid (nhead_q, batch, tiles): every batch's heaviest M-tiles start first)
+// instead of batch after batch, while the K/V one XCD serves stays within
+// twice an MI355X XCD's 4 MiB L2.  Heads go to the XCDs round robin, so an
+// XCD serves batch x ceil(nhead_k / 8) x seqlen_k x 256 bytes of K/V.  Beyond
+// that the interleaved batches push each sequence's K/V out of L2 before its
+// later M-tiles run.  Measured on causal grids (regular form): +19% B8 H16
+// S1024, +8% B4 H16 S2048, +6% B16 H8 S2048, +2-6% B2 H16 S4096/S8192, and
+// -1 to -5% above 8 MiB.
+bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
+    if (!causal || batch < 2 || p->seqstart_q != nullptr) return false;
+    const int64_t kv_bytes_per_xcd = (int64_t)batch * ((p->nhead_k + 7) / 8) * p->seqlen_k * 256;
+    return kv_bytes_per_xcd <= ((int64_t)8 << 20);
+}
+
 // blocks of the regular grid and of the pair grid
 int64_t grid_blocks(const FmhaFwdParams* p, int batch) {
     return (int64_t)p->nhead_q * ((p->seqlen_q + kM0 - 1) / kM0) * batch;
@@ -118,10 +133,17 @@ extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch,
                         compute_units > 0 ? compute_units : device_cus());
 }
 
+extern "C" int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* p, int batch, int causal) {
+    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
+    return use_tilemajor(p, batch, causal) ? 1 : 0;
+}
+
 extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batch, int causal, int variant,
                                                 hipStream_t stream) {
     const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
     if (chk != hipSuccess) return chk;
+    const bool tile_major = (variant & FMHA_VARIANT_REFERENCE_ORDER) == 0 && use_tilemajor(p, batch, causal);
+    variant &= ~FMHA_VARIANT_REFERENCE_ORDER;
     if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_PAIR) return hipErrorInvalidValue;
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
@@ -129,6 +151,18 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     const bool varlen = p->seqstart_q != nullptr;
     if (variant == FMHA_VARIANT_AUTO)
         variant = pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus());
+    if (tile_major) {  // causal, dense, batch > 1
+        if (variant == FMHA_VARIANT_PAIR)
+            hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk1_tilemajor, dim3(p->nhead_q, batch, (m_tiles + 1) / 2),
+                               dim3(FMHA_SPLIT_KBLOCK), 0, stream, *p);
+        else if (variant == FMHA_VARIANT_SPLITKV)
+            hipLaunchKernelGGL(fmha_fwd_d64_bf16_splitkv_msk1_tilemajor, dim3(p->nhead_q, batch, m_tiles),
+                               dim3(FMHA_SPLIT_KBLOCK), 0, stream, *p);
+        else
+            hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk1_tilemajor, dim3(p->nhead_q, batch, m_tiles), dim3(kBlockSize),
+                               0, stream, *p);
+        return hipGetLastError();
+    }
     if (variant == FMHA_VARIANT_PAIR) {
         const dim3 pgrid(p->nhead_q, (m_tiles + 1) / 2, batch);
         const dim3 block(FMHA_SPLIT_KBLOCK);

@@ -755,3 +755,23 @@ FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
     fwd_mtile<true, true, kModePair>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, ring);
 }
+
+// ---- tile-major causal entries (this build's own; no counterpart in the
+// reference): the causal dense entries of the three forms on the grid
+// (nhead_q, batch, tiles), tiles = the M-tiles (pairs for the pair form) of a
+// (batch, head).  Blocks are dispatched x fastest, then y, then z, so every
+// batch's heaviest M-tiles start before any lighter one, instead of batch
+// after batch.  Each index comes straight from one grid coordinate: these
+// entries never branch on the grid's shape. ----
+FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_tilemajor(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, false, kModeRegular>(params, blockIdx.y, blockIdx.x, gridDim.z - 1 - blockIdx.z, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1_tilemajor(FmhaFwdParams params) {
+    FMHA_RING(ring, 2 * kTileBytes)
+    fwd_mtile<true, false, kModeSplitKV>(params, blockIdx.y, blockIdx.x, gridDim.z - 1 - blockIdx.z, ring);
+}
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1_tilemajor(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    fwd_mtile<true, false, kModePair>(params, blockIdx.y, blockIdx.x, gridDim.z - 1 - blockIdx.z, ring);
+}

@@ -122,12 +122,17 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
  *                         per two adjacent M-tiles of a (batch, head)
- * All forms give the same results up to fp32 rounding order.  An unknown
+ * All forms give the same results up to fp32 rounding order.  Causal dense
+ * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
+ * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
+ * (every batch's heaviest M-tiles first) unless FMHA_VARIANT_REFERENCE_ORDER
+ * is OR-ed into `variant`; the order changes no result bit.  An unknown
  * variant returns hipErrorInvalidValue. */
 #define FMHA_VARIANT_AUTO 0
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
 #define FMHA_VARIANT_PAIR 3
+#define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
 
@@ -140,6 +145,12 @@ hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int c
  * launching (this build's own; no counterpart in the reference).  Returns
  * FMHA_VARIANT_REGULAR, _SPLITKV or _PAIR, or -1 for rejected arguments. */
 int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* params, int batch, int causal, int compute_units);
+
+/* 1 when a launch with these arguments (without FMHA_VARIANT_REFERENCE_ORDER)
+ * runs a tile-major entry, 0 when it keeps the reference's order, -1 for
+ * rejected arguments; host only (this build's own; no counterpart in the
+ * reference). */
+int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* params, int batch, int causal);
 
 /* Tile constants of the linked library, so FFI callers (ctypes, cgo) need not
  * parse this header: writes kM0, kN0, kBlockSize, head dim. */
@@ -211,6 +222,13 @@ __global__ void fmha_fwd_d64_bf16_pair_msk0(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params);
+/* Tile-major causal dense forms (no counterpart in the reference): grid
+ * (nhead_q, batch, tiles), tiles = ceil(seqlen_q/kM0) (pair form: pairs of
+ * them), block kBlockSize (regular) or FMHA_SPLIT_KBLOCK; block z runs M-tile
+ * (pair) tiles-1-z, so all batches' heaviest M-tiles are dispatched first. */
+__global__ void fmha_fwd_d64_bf16_msk1_tilemajor(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_splitkv_msk1_tilemajor(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_pair_msk1_tilemajor(FmhaFwdParams params);
 #endif
 #endif /* __cplusplus */
 

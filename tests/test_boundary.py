@@ -29,7 +29,7 @@ REFERENCE_OFFSETS = {
 KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_d64_bf16_msk0_varlen",
                   "fmha_fwd_d64_bf16_msk1_varlen"]
 SPLIT_ENTRIES = [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("splitkv", "pair") for m in (0, 1)
-                 for v in ("", "_varlen")]
+                 for v in ("", "_varlen")] + [f"fmha_fwd_d64_bf16_{f}msk1_tilemajor" for f in ("", "splitkv_", "pair_")]
 
 
 def header_c_functions():
@@ -176,7 +176,8 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    for bad in (-1, 4, 100):  # 0-3 are the valid forms
+    # 0-3 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
+    for bad in (-1, 4, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 4):
         assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
     bad_p = _mut(q=None)
     assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID
@@ -220,6 +221,35 @@ def test_auto_form_rule(batch, heads, seqlen, causal, cus, form):
     """The launcher's documented rule (grid shape -> kernel form), host only."""
     p, b = _shape(batch, heads, seqlen)
     assert fmha.pick_variant(p, b, causal, cus) == form
+
+
+@pytest.mark.parametrize("batch,heads,kv_heads,seqlen,causal,varlen,expect", [
+    (8, 16, 16, 1024, 1, False, 1),    # 8 x 2 x 1024 x 256 B = 4 MiB per XCD
+    (4, 16, 16, 2048, 1, False, 1),    # 4 MiB
+    (16, 8, 8, 2048, 1, False, 1),     # 8 MiB: the limit itself
+    (16, 16, 16, 2048, 1, False, 0),   # 16 MiB
+    (4, 32, 32, 4096, 1, False, 0),    # 16 MiB
+    (16, 16, 2, 2048, 1, False, 1),    # GQA: 2 K/V heads are at most one per XCD -> 8 MiB
+    (17, 16, 2, 2048, 1, False, 0),    # 8.5 MiB
+    (1, 16, 16, 8192, 1, False, 0),    # one batch: nothing to interleave
+    (8, 16, 16, 1024, 0, False, 0),    # dense: every block costs the same
+    (8, 16, 16, 1024, 1, True, 0),     # varlen keeps the reference's order
+])
+def test_tile_major_rule(batch, heads, kv_heads, seqlen, causal, varlen, expect):
+    """Causal dense batches run tile-major while the K/V one XCD serves,
+    batch x ceil(nhead_k/8) x seqlen_k x 256 bytes, is at most 8 MiB."""
+    p = valid_params(lse=False)
+    p.nhead_q, p.nhead_k = heads, kv_heads
+    p.seqlen_q = p.seqlen_k = seqlen
+    if varlen:
+        seq = (ctypes.c_int32 * 2)(0, seqlen)
+        p.seqstart_q = p.seqstart_k = ctypes.cast(seq, ctypes.c_void_p).value
+    assert fmha.tile_major(p, batch, causal) == expect
+
+
+def test_tile_major_rejects_what_the_launch_rejects():
+    assert fmha.tile_major(_mut(q=None), 2, 1) == -1
+    assert fmha.tile_major(valid_params(), 2, 2) == -1
 
 
 def test_auto_form_rejects_what_the_launch_rejects():

@@ -123,9 +123,10 @@ def test_varlen_equals_per_sequence_dense_bitwise(form):
 @pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("seqlen,heads", [(700, 8), (11000, 8)])
 def test_causal_batch_equals_single_batches_bitwise(form, seqlen, heads):
-    """A causal grid with several batches (heaviest M-tiles first within each
-    batch) gives each batch the bits of a batch-1 launch of its own, for short
-    and long sequences (3 x 700 and 3 x 11,000 keys)."""
+    """A causal grid with several batches gives each batch the bits of a
+    batch-1 launch of its own, for short and long sequences: 3 x 700 keys run
+    on the tile-major entries, 3 x 11,000 keys (8.4 MB of K/V per XCD) batch
+    after batch."""
     b = 3
     pb = Problem(batch=b, nhead_q=heads, seqlen_q=seqlen, causal=True, lse=True)
     q, k, v = make_inputs(pb, "normal", 21)
@@ -137,6 +138,34 @@ def test_causal_batch_equals_single_batches_bitwise(form, seqlen, heads):
                             v[i * per * 64:(i + 1) * per * 64], variant=FORMS[form])
         assert np.array_equal(o1, ob[i * per * 64:(i + 1) * per * 64]), i
         assert np.array_equal(l1, lb[i * per:(i + 1) * per]), i
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("batch,heads,kv_heads,seqlen_q,seqlen_k", [
+    (3, 8, 8, 700, 700), (4, 4, 2, 384, 1000), (2, 2, 1, 1000, 333), (5, 3, 1, 129, 129), (2, 8, 8, 2048, 2048)])
+def test_tile_major_order_equals_reference_order_bitwise(form, batch, heads, kv_heads, seqlen_q, seqlen_k):
+    """Causal dense batches run on the tile-major entries (grid (nhead_q,
+    batch, tiles), every batch's heaviest M-tiles first); each block computes
+    the same M-tile with the same arithmetic as in the reference's
+    batch-after-batch order, so O and LSE match that order bit for bit."""
+    import torch
+
+    from harness import build_params
+
+    pb = Problem(batch=batch, nhead_q=heads, nhead_k=kv_heads, seqlen_q=seqlen_q, seqlen_k=seqlen_k, causal=True,
+                 lse=True)
+    nq, nk, nlse = pb.sizes()
+    host = [torch.empty(n, dtype=torch.int16) for n in (nq, nk, nk, nq)]
+    p = build_params(pb, *host, torch.empty(nlse, dtype=torch.float32), None)
+    assert fmha.tile_major(p, batch, 1) == 1  # the default launch takes the tile-major entry
+    q, k, v = make_inputs(pb, "normal", 31)
+    o_tm, l_tm = run_kernel(pb, q, k, v, variant=FORMS[form])
+    o_ref, l_ref = run_kernel(pb, q, k, v, variant=FORMS[form] | fmha.VARIANT_REFERENCE_ORDER)
+    assert np.array_equal(o_tm, o_ref)
+    assert np.array_equal(l_tm, l_ref)
+    o_ora, l_ora = oracle.run(pb, q, k, v)
+    assert verify.baseline_rule(o_ora, verify.bf16_bits_to_f32(o_tm))["pass"]
+    assert verify.lse_rule(l_ora, l_tm)["pass"]
 
 
 @pytest.mark.parametrize("form", list(FORMS))
