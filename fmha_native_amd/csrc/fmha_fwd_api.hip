@@ -92,11 +92,12 @@ int device_cus() {
 //    causal at >= 32768; with a partial last round it loses 8-17%.
 //  * regular: everything else (the dense B4 H16 S2048 and causal B1 H16 S8192
 //    benchmark grids among them).
-int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int cus) {
+int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_t cus) {
     if (FMHA_SPLIT_POLICY == 0) return FMHA_VARIANT_REGULAR;
     if (FMHA_SPLIT_POLICY == 1) return FMHA_VARIANT_SPLITKV;
+    // blocks (up to ~2^63) is only compared, never multiplied; cus < 2^31
     if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
-    if (causal && (2 * blocks <= 3 * cus || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
+    if (causal && (blocks <= 3 * cus / 2 || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
     const bool whole_rounds = pairs >= cus && pairs % cus == 0;
     if (whole_rounds && seqlen_k >= (causal ? 32768 : 8192)) return FMHA_VARIANT_PAIR;
     return FMHA_VARIANT_REGULAR;
@@ -113,8 +114,10 @@ int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int cu
 // -1 to -5% above 8 MiB.
 bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     if (!causal || batch < 2 || p->seqstart_q != nullptr) return false;
-    const int64_t kv_bytes_per_xcd = (int64_t)batch * ((p->nhead_k + 7) / 8) * p->seqlen_k * 256;
-    return kv_bytes_per_xcd <= ((int64_t)8 << 20);
+    // batch x heads-per-XCD x seqlen_k <= 8 MiB / 256 B, evaluated without overflow
+    const int64_t limit = ((int64_t)8 << 20) / 256;
+    const int64_t rows = (int64_t)batch * (((int64_t)p->nhead_k + 7) / 8);  // <= 2^16 * 2^28
+    return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
 // blocks of the regular grid and of the pair grid

@@ -247,6 +247,19 @@ def test_tile_major_rule(batch, heads, kv_heads, seqlen, causal, varlen, expect)
     assert fmha.tile_major(p, batch, causal) == expect
 
 
+def test_rules_at_extreme_counts():
+    """Head and CU counts near INT_MAX: the rules stay defined and monotone."""
+    big = 2**31 - 1
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = big
+    assert fmha.tile_major(p, 65535, 1) == 0
+    assert fmha.pick_variant(p, 65535, 1, 256) == R
+    q = valid_params(lse=False)
+    assert fmha.pick_variant(q, 1, 1, big) == S       # every grid fits such a device at once
+    q.seqlen_k = 0
+    assert fmha.tile_major(q, 65535, 1) == 1          # no K/V at all
+
+
 def test_tile_major_rejects_what_the_launch_rejects():
     assert fmha.tile_major(_mut(q=None), 2, 1) == -1
     assert fmha.tile_major(valid_params(), 2, 2) == -1
