@@ -138,6 +138,7 @@ extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch,
 
 extern "C" int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* p, int batch, int causal) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
+    if (p->seqlen_q == 0) return 0;  // nothing is launched
     return use_tilemajor(p, batch, causal) ? 1 : 0;
 }
 

@@ -260,6 +260,12 @@ def test_rules_at_extreme_counts():
     assert fmha.tile_major(q, 65535, 1) == 1          # no K/V at all
 
 
+def test_tile_major_only_when_something_is_launched():
+    p = valid_params(lse=False)
+    p.seqlen_q = 0
+    assert fmha.tile_major(p, 4, 1) == 0
+
+
 def test_tile_major_rejects_what_the_launch_rejects():
     assert fmha.tile_major(_mut(q=None), 2, 1) == -1
     assert fmha.tile_major(valid_params(), 2, 2) == -1
