@@ -4,7 +4,8 @@
   rows (16,776,000 keys: (rows + 192) * 128 bytes + 256 < 2^31), dense and
   bottom-right causal, in the automatic form and the reference-named entries;
 * the largest grid y: 65,535 M-tiles (seqlen_q = 65,535 * 128);
-* the largest grid z: 65,535 batches;
+* the largest grid z: 65,535 batches, and the tile-major grid with the most
+  batches in y that its 8 MiB rule allows (32,768);
 * thousands of varlen sequences, some of them empty.
 
 Each is checked against a float64 numpy evaluation of sampled rows
@@ -126,13 +127,27 @@ def test_largest_grid_y(causal):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_largest_grid_z(causal):
+    _many_batches(65535, 3, causal, tile_major=0)
+
+
+@pytest.mark.parametrize("b,s", [(32768, 1), (10922, 3)])
+def test_largest_tile_major_grid(b, s):
+    """Causal batches at the tile-major rule's limit (b x s K/V rows of one
+    head per XCD = 32,768 or 32,766, i.e. 8 MiB): grid (2, b, tiles)."""
+    _many_batches(b, s, True, tile_major=1)
+
+
+def _many_batches(b, s, causal, tile_major):
     import torch
 
-    b, hq, hk, s = 65535, 2, 1, 3
+    hq, hk = 2, 1
     g = torch.Generator(device="cuda").manual_seed(13)
     q = torch.randn((b, hq, s, 64), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
     k = torch.randn((b, hk, s, 64), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
     v = torch.randn((b, hk, s, 64), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    ls = torch.empty(q.shape[:-1], dtype=torch.float32, device=q.device)
+    assert fmha.tile_major(fmha.params_from_tensors(q, k, v, o, ls), b, int(causal)) == tile_major
     o, ls = _run(q, k, v, causal, fmha.VARIANT_AUTO)
     qf, kf, vf = _f64(q), _f64(k)[:, [0, 0]], _f64(v)[:, [0, 0]]  # GQA: both q heads read kv head 0
     sc = np.einsum("bhid,bhjd->bhij", qf, kf) * SCALE
