@@ -7,14 +7,20 @@ causal; reference src/bench_fmha_fwd.cpp:225-226) and its fraction of the
 MI355X dense BF16 MFMA peak (2516.6 TFLOP/s).  ``value`` is measured on the
 dense B4 H16 S2048 configuration; the causal B1 H16 S8192 (+LSE)
 configuration is reported under ``also``.  A step is one launch of the
-forward over the whole batch with Q/K/V already resident in HBM.  Inputs are
-synthetic N(0,1) bf16 (seed 42).
+forward over the whole batch with Q/K/V already resident in HBM, timed with
+the reference's protocol (HIP events around each launch); the back-to-back
+average of as many launches is reported beside it.  Inputs are synthetic
+N(0,1) bf16 (seed 42).
+
+``roofline`` carries this run's achieved TFLOP/s and, from the committed
+rocprofv3 run of the same kernel (profiles/), its HBM traffic, MFMA busy
+fraction and clock.
 
 The CPU baseline is the reference's own CPU path, cpu_ref_verify, compiled
-from its sources into oracle/_ref/ref_verify and timed over the whole dense
-workload on this host ("kind": "reference"); where that harness was not built,
-the faithful C restatement (oracle/) on a bounded row sample ("kind": "port").
-Only this leg touches oracle/.
+from its sources into oracle/_ref/ref_verify and timed over the whole
+workload of both metric configurations on this host ("kind": "reference");
+where that harness was not built, the faithful C restatement (oracle/) on a
+bounded row sample ("kind": "port").  Only this leg touches oracle/.
 """
 import argparse
 import json
@@ -73,58 +79,144 @@ def _params(prob, dq, dk, dv, do, dlse, dseq=None):
     return p
 
 
+class _HipEvents:
+    """hipEventCreate/Record/Synchronize/ElapsedTime through ctypes, on the
+    HIP runtime torch already loaded (one runtime per process: dlopen by its
+    soname returns the loaded copy).  Recording through ctypes keeps the host
+    time between an event and the launch it brackets to the launcher's own
+    cost, as in the reference's C++ loop."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        vp = ctypes.c_void_p
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        self.lib.hipEventRecord.argtypes = [vp, vp]
+        self.lib.hipEventSynchronize.argtypes = [vp]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        self.lib.hipEventDestroy.argtypes = [vp]
+
+    def create(self, n):
+        evs = []
+        for _ in range(n):
+            e = self.ct.c_void_p()
+            assert self.lib.hipEventCreate(self.ct.byref(e)) == 0, "hipEventCreate"
+            evs.append(e)
+        return evs
+
+    def elapsed_ms(self, e0, e1):
+        ms = self.ct.c_float()
+        assert self.lib.hipEventElapsedTime(self.ct.byref(ms), e0, e1) == 0, "hipEventElapsedTime"
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
+
+
 def time_problem(prob, steps, warmup, torch, mult=1.0):
-    """Warm up, then time exactly `steps` back-to-back launches on torch's
-    current stream with HIP events recorded on that same stream."""
+    """Warm up, then time exactly `steps` launches with the reference's
+    protocol (src/bench_fmha_fwd.cpp:204-210): HIP events recorded on the
+    launch stream right before and after each launch, synchronised per
+    launch, times averaged.  Then the same number of launches back to back
+    between two events (launch gaps hidden), reported beside it."""
+    import ctypes
+
     import fmha_native_amd as fmha
 
     host, (dq, dk, dv), do, dlse, dseq = _device_inputs(prob, torch, mult=mult)
     p = _params(prob, dq, dk, dv, do, dlse, dseq)
     stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    launch = fmha.load_library().fmha_fwd_d64_bf16
+    pp, batch, causal = ctypes.byref(p), prob.batch, int(prob.causal)
+    hip = _HipEvents()
     for _ in range(warmup):
-        fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), sh)
+        assert launch(pp, batch, causal, sh) == 0
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0, e1 = hip.create(2)
+    times = []
     t0 = time.perf_counter()
-    e0.record(stream)
     for _ in range(steps):
-        fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), sh)
-    e1.record(stream)
+        hip.lib.hipEventRecord(e0, sh)
+        rc = launch(pp, batch, causal, sh)
+        hip.lib.hipEventRecord(e1, sh)
+        hip.lib.hipEventSynchronize(e1)
+        assert rc == 0, f"launch returned {rc}"
+        times.append(hip.elapsed_ms(e0, e1))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / steps
-    return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "host": host}
+    ms = sum(times) / steps
+    hip.lib.hipEventRecord(e0, sh)
+    for _ in range(steps):
+        launch(pp, batch, causal, sh)
+    hip.lib.hipEventRecord(e1, sh)
+    torch.cuda.synchronize()
+    b2b = hip.elapsed_ms(e0, e1) / steps
+    hip.destroy([e0, e1])
+    return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12,
+            "b2b_ms": b2b, "b2b_tflops": prob.flops() / (b2b * 1e-3) / 1e12, "host": host}
 
 
 REF_VERIFY = os.path.join(ROOT, "oracle", "_ref", "ref_verify")
 
 
+def _host_threads():
+    """(nproc, OMP_NUM_THREADS or None, threads OpenMP will use)."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = int(omp) if omp and omp.isdigit() and int(omp) > 0 else nproc
+    return nproc, omp, threads
+
+
 def cpu_baseline_reference(prob):
     """The reference's own CPU path, cpu_ref_verify (src/runner/cpu_ref.cpp:14-311,
     compiled from its sources into oracle/_ref/ref_verify), over the whole
-    workload, timed by the harness around that one call.  None if not built."""
+    workload, timed by the harness around that one call.  Its loop nest
+    (cpu_ref.cpp:73-84) is OpenMP over (batch, head) rows and computes every
+    (query, key) score, masked ones included, so a causal problem costs it the
+    dense work.  None if not built."""
     import subprocess
 
-    if not os.path.exists(REF_VERIFY) or prob.causal or prob.lse:
+    if not os.path.exists(REF_VERIFY) or prob.varlen:
         return None
-    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(prob.nhead_q), "-s", str(prob.seqlen_q), "--seed", "42"]
-    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(prob.nhead_q), "-s", str(prob.seqlen_q), "--seed", "42",
+           "--mask", str(int(prob.causal)), "--lse", str(int(prob.lse))]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         return None
     res = [json.loads(l.split(" ", 1)[1]) for l in r.stdout.splitlines() if l.startswith("REF_VERIFY ")]
     if not res:
         return None
     t, thr = res[0]["cpu_ref_seconds"], res[0]["threads"]
+    nproc, omp, _ = _host_threads()
+    units = prob.batch * prob.nhead_q
+    # collapse(2) schedule(dynamic, 16) hands out the B*H (batch, head) units
+    # 16 at a time: ceil(B*H / 16) chunks, so at most that many threads work
+    chunks = -(-units // 16)
+    lse = f", LSE |d| max {res[0]['lse_max_abs']:.2e}" if prob.lse else ""
     return {
         "value": prob.flops() / t / 1e12,
         "unit": "TFLOP/s",
         "cores": thr,
         "kind": "reference",
-        "sample": f"the reference's cpu_ref_verify over the full B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q} "
-                  f"workload (its fill_random(42) inputs; time does not depend on values), {t:.2f} s on {thr} "
-                  f"OpenMP threads; its check of this kernel's O: pass={res[0]['pass']}",
+        "seconds": round(t, 3),
+        "nproc": nproc,
+        "omp_num_threads": omp,
+        "effective_parallelism": min(thr, chunks),
+        "sample": f"the reference's cpu_ref_verify over the full B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}"
+                  f"{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''} workload (its fill_random(42) "
+                  f"inputs; time does not depend on values), {t:.2f} s on {thr} OpenMP threads, of which "
+                  f"min({thr}, ceil(B*H/16) = {chunks}) = {min(thr, chunks)} have work (its loop is collapse(2) "
+                  f"schedule(dynamic, 16) over the B*H = {units} (batch, head) units, cpu_ref.cpp:73-84); FLOPs "
+                  f"by the repo convention"
+                  f"{' (x0.5; the loop computes every masked score too)' if prob.causal else ''}; its check of "
+                  f"this kernel's output: pass={res[0]['pass']}{lse}",
     }
 
 
@@ -132,8 +224,8 @@ def cpu_baseline(prob, host, budget_s=10.0):
     """Reference-faithful oracle on rows [0, R) of every (batch, head)."""
     import oracle
 
-    nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    nthreads = max(1, min(nthreads, prob.batch * prob.nhead_q))  # reference parallelises over (b, h)
+    nproc, omp, threads = _host_threads()
+    nthreads = max(1, min(threads, prob.batch * prob.nhead_q))  # reference parallelises over (b, h)
     q, k, v = host
 
     def run(rows):
@@ -146,25 +238,57 @@ def cpu_baseline(prob, host, budget_s=10.0):
     while t < 0.5 * budget_s and rows < prob.seqlen_q:  # grow the sample to ~budget_s
         rows = int(min(prob.seqlen_q, max(rows + 1, rows * 0.9 * budget_s / max(t, 1e-3))))
         t = run(rows)
-    flops = 4.0 * 64 * prob.seqlen_k * rows * prob.batch * prob.nhead_q
+    # the loop nest computes every key of every sampled row, masked or not
+    flops = 4.0 * 64 * prob.seqlen_k * rows * prob.batch * prob.nhead_q * (0.5 if prob.causal else 1.0)
     return {
         "value": flops / t / 1e12,
         "unit": "TFLOP/s",
         "cores": nthreads,
         "kind": "port",
+        "seconds": round(t, 3),
+        "nproc": nproc,
+        "omp_num_threads": omp,
+        "effective_parallelism": min(nthreads, -(-(prob.batch * prob.nhead_q) // 16)),  # dynamic,16 chunks
         "sample": f"faithful C oracle, query rows [0,{rows}) of all {prob.batch * prob.nhead_q} (b,h) of "
-                  f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q} (full keys), {t:.1f} s on {nthreads} threads",
+                  f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}{' causal' if prob.causal else ''} (full keys), "
+                  f"{t:.1f} s on {nthreads} threads; extrapolated to the whole workload at that rate",
     }
 
 
-def _traffic():
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
+PROFILE_JSON = os.path.join(ROOT, "profiles", "roofline_fmha_fwd_d64_bf16_cfg2_cfg3.json")
+
+
+def _profile(workload):
+    """Counter figures for ``workload`` from the committed rocprofv3 run
+    (profiles/, written by ``python -m fmha_native_amd.rocprof``), or None."""
     try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+        with open(PROFILE_JSON) as f:
+            return json.load(f).get(workload)
     except (OSError, ValueError):
         return None
+
+
+def _roofline(achieved, workload):
+    """The roofline object: ``achieved``/``frac`` from this run's HIP events;
+    HBM traffic, MFMA busy and the clock from the committed rocprofv3 run of
+    the same kernel (one box, one process tree), where
+    frac_from_counters = mfma_busy x clock / 2.4 GHz checks the timer."""
+    prof = _profile(workload)
+    r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+         "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    if prof:
+        r.update({
+            "traffic": prof["hbm_bytes_per_launch"],
+            "algorithmic_bytes": prof["algorithmic_bytes"],
+            "mfma_busy": prof["mfma_busy"],
+            "clock_ghz": prof["clock_ghz"],
+            "frac_from_counters": prof["frac_from_counters"],
+            "profile": {"file": os.path.relpath(PROFILE_JSON, ROOT), "kernel": prof["kernel"],
+                        "trace_avg_us": prof["trace_avg_us"], "bench_ms_per_step_same_box": prof["bench_ms_per_step"],
+                        "note": "traffic, mfma_busy and clock_ghz come from that run; this line's frac is timed on "
+                                "this box, whose clock under load may differ (frac ~ mfma_busy x clock / 2.4 GHz)"},
+        })
+    return r
 
 
 def main():
@@ -203,7 +327,8 @@ def main():
     if args.only:
         prob = cfg2 if args.only == "cfg2" else cfg3
         r = time_problem(prob, args.steps, args.warmup, torch)
-        print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"]}), flush=True)
+        print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"],
+                          "back_to_back_ms": r["b2b_ms"]}), flush=True)
         return
     r2 = time_problem(cfg2, args.steps, args.warmup, torch)
     r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)
@@ -216,7 +341,8 @@ def main():
             prob, mult = baseline_problems()[name]
             r = time_problem(prob, max(1, args.steps // 4), max(1, args.warmup // 2), torch, mult)
             e = {"workload": prob.name, "ms_per_step": round(r["ms"], 5), "value": round(r["tflops"], 2),
-                 "pct_bf16_peak": round(100.0 * r["tflops"] / PEAK_BF16_TFLOPS, 2)}
+                 "pct_bf16_peak": round(100.0 * r["tflops"] / PEAK_BF16_TFLOPS, 2),
+                 "back_to_back": {"ms_per_step": round(r["b2b_ms"], 5), "value": round(r["b2b_tflops"], 2)}}
             if prob.varlen:
                 e["value_exact_flops"] = round(prob.exact_flops() / (r["ms"] * 1e-3) / 1e12, 2)
                 e["note"] = ("value uses the repo FLOP convention (max S for every sequence, an overcount); "
@@ -229,6 +355,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_reference(cfg2) or cpu_baseline(cfg2, r2["host"])
+        c3 = cpu_baseline_reference(cfg3) or cpu_baseline(cfg3, r3["host"])
+        cpu["cfg3"] = {k: c3[k] for k in ("value", "unit", "cores", "kind", "seconds", "effective_parallelism",
+                                          "sample")}
 
     achieved = r2["tflops"]
     line = {
@@ -245,23 +374,21 @@ def main():
         "vs_baseline_note": "ratio to the reference's published MI300X figure for this config (348.4 TFLOP/s, "
                             "README.md:91); no MI355X figure is published",
         "pct_bf16_peak": round(100.0 * achieved / PEAK_BF16_TFLOPS, 2),
+        "timing": "per launch, HIP events around each launch on its stream (src/bench_fmha_fwd.cpp:204-210), "
+                  "averaged over the timed steps",
+        "back_to_back": {"ms_per_step": round(r2["b2b_ms"], 5), "value": round(r2["b2b_tflops"], 2)},
         "dtype": "bf16",
         "data": "synthetic: Q/K/V i.i.d. N(0,1) bf16, seed 42 (fill_normal)",
         "config": {"workload": "dense MHA forward B4 H16 Sq=Sk=2048 D64, no mask, no LSE, BHSD",
                    "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False, "lse": False},
-        "roofline": {
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": _traffic(),
-        },
+        "roofline": _roofline(achieved, "cfg2"),
         "also": {
             "workload": "causal MHA forward B1 H16 Sq=Sk=8192 D64 with LSE (FLOPs x0.5)",
             "ms_per_step": round(r3["ms"], 5),
             "value": round(r3["tflops"], 2),
             "pct_bf16_peak": round(100.0 * r3["tflops"] / PEAK_BF16_TFLOPS, 2),
+            "back_to_back": {"ms_per_step": round(r3["b2b_ms"], 5), "value": round(r3["b2b_tflops"], 2)},
+            "roofline": _roofline(r3["tflops"], "cfg3"),
             "vs_reference_mi300x": round(r3["tflops"] / 358.1, 3),
         },
         "others": others,

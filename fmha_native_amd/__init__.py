@@ -37,6 +37,7 @@ HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 HEAD_DIM = 64
 MERGE_MAX_PARTS = 64
+INT32_MAX = 2**31 - 1
 
 
 class FmhaError(RuntimeError):
@@ -182,7 +183,20 @@ def varlen_lengths(seed, n, lo, hi):
     return list(out)
 
 
-def _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q):
+def _check_kernarg_ints(q, k, v, o, max_seqlen_q, max_seqlen_k):
+    """Every kernarg integer is a C int: reject a value that would wrap instead
+    of letting ctypes truncate it silently (a wrapped stride can come out
+    positive, pass every check and alias another batch or head)."""
+    ints = {"max_seqlen_q": max_seqlen_q, "max_seqlen_k": max_seqlen_k}
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        ints[f"{name}.shape"] = max(t.shape)
+        ints.update({f"{name}.stride({d})": t.stride(d) for d in range(t.dim())})
+    for name, val in ints.items():
+        if val is not None and not 0 <= int(val) <= INT32_MAX:
+            raise ValueError(f"{name} = {val} does not fit the kernarg's 32-bit int")
+
+
+def _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q, max_seqlen_k=None):
     import torch
 
     varlen = seqstart_q is not None
@@ -214,6 +228,11 @@ def _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q):
     if lse is not None:
         if lse.dtype != torch.float32 or tuple(lse.shape) != tuple(q.shape[:-1]) or not lse.is_contiguous():
             raise ValueError(f"lse must be a contiguous float32 tensor of shape {tuple(q.shape[:-1])}")
+        if varlen and q.stride(0) != q.shape[1] * q.stride(1):
+            # the kernel addresses varlen LSE rows as h * (nhead_stride_q / stride_q) + token
+            # (include/fmha_fwd.h), so q's head stride must be exactly T rows
+            raise ValueError("varlen LSE needs q's head stride to be T rows (q.stride(0) == q.shape[1] * q.stride(1))")
+    _check_kernarg_ints(q, k, v, o, max_seqlen_q, max_seqlen_k)
     tensors = [q, k, v, o] + [t for t in (lse, seqstart_q, seqstart_k) if t is not None]
     if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
         raise ValueError("all tensors must be on the same GPU")
@@ -228,14 +247,16 @@ def params_from_tensors(q, k, v, o, lse=None, seqstart_q=None, seqstart_k=None, 
     [Hq, T, 64], k/v [Hk, T, 64], with int32 ``seqstart_*`` of batch+1 entries.
     ``lse``: float32, [B, Hq, Sq] (dense) or [Hq, T] (varlen), contiguous.
     Raises ValueError for tensors the kernel cannot take (dtype, rank, head
-    dim, inner stride, mismatched shapes, or memory that is not on one GPU).
+    dim, inner stride, mismatched shapes, a varlen q whose head stride is not
+    T rows while LSE is written, a size or stride outside the kernarg's 32-bit
+    ints, or memory that is not on one GPU).
     """
-    _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q)
+    _check_tensors(q, k, v, o, lse, seqstart_q, seqstart_k, max_seqlen_q, max_seqlen_k)
+    varlen = seqstart_q is not None
     p = FmhaFwdParams()
     p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     p.lse = lse.data_ptr() if lse is not None else None
     p.scale = LOG2E / math.sqrt(HEAD_DIM) if scale is None else float(scale)
-    varlen = seqstart_q is not None
     if varlen:
         p.nhead_q, p.nhead_k = q.shape[0], k.shape[0]
         p.seqlen_q = int(max_seqlen_q)
@@ -296,14 +317,26 @@ def merge_partials(o_parts, lse_parts, o=None, lse=None, stream=None):
     """
     import torch
 
+    if o_parts.dtype not in (torch.bfloat16, torch.int16) or lse_parts.dtype != torch.float32:
+        raise ValueError("o_parts must be bfloat16 (or int16 bf16 bits) and lse_parts float32")
+    if o_parts.dim() < 2 or o_parts.shape[-1] != HEAD_DIM or tuple(o_parts.shape[:-1]) != tuple(lse_parts.shape):
+        raise ValueError(f"o_parts {tuple(o_parts.shape)} must be [n, ..., {HEAD_DIM}] over lse_parts "
+                         f"{tuple(lse_parts.shape)} = [n, ...]")
+    if not (o_parts.is_contiguous() and lse_parts.is_contiguous()):
+        raise ValueError("o_parts and lse_parts must be contiguous")
     n = o_parts.shape[0]
     rows = lse_parts[0].numel()
-    if not (o_parts.is_contiguous() and lse_parts.is_contiguous()) or o_parts[0].numel() != rows * HEAD_DIM:
-        raise ValueError("o_parts [n, ..., 64] and lse_parts [n, ...] must be contiguous and agree")
     if o is None:
         o = torch.empty(o_parts.shape[1:], dtype=o_parts.dtype, device=o_parts.device)
+    elif o.dtype != o_parts.dtype or tuple(o.shape) != tuple(o_parts.shape[1:]) or not o.is_contiguous():
+        raise ValueError(f"o must be a contiguous {o_parts.dtype} tensor of shape {tuple(o_parts.shape[1:])}")
     if lse is None:
         lse = torch.empty(lse_parts.shape[1:], dtype=torch.float32, device=lse_parts.device)
+    elif lse.dtype != torch.float32 or tuple(lse.shape) != tuple(lse_parts.shape[1:]) or not lse.is_contiguous():
+        raise ValueError(f"lse must be a contiguous float32 tensor of shape {tuple(lse_parts.shape[1:])}")
+    tensors = (o_parts, lse_parts, o, lse)
+    if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
+        raise ValueError("all tensors must be on the same GPU")
     if stream is None:
         stream = torch.cuda.current_stream(o_parts.device).cuda_stream
     fmha_merge_d64_bf16(n, rows, o_parts.data_ptr(), rows * HEAD_DIM, lse_parts.data_ptr(), rows, HEAD_DIM,

@@ -5,7 +5,6 @@
 Outputs (git-ignored, but shipped to the GPU box with the tree):
   fmha_native_amd/libfmha_native_amd.so   kernels + C-ABI launcher + input generators
   fmha_native_amd/bench_fmha_fwd          the timing CLI
-  fmha_native_amd/probe_coissue           the VALU/MFMA co-issue microbenchmark
   oracle/liboracle.so                     CPU oracle (test infrastructure only)
 
 Every HIP source is compiled for gfx950 only, with packed-FP32 instruction
@@ -37,7 +36,6 @@ HIP_FLAGS = [
 
 LIB = os.path.join(PKG, "libfmha_native_amd.so")
 BENCH = os.path.join(PKG, "bench_fmha_fwd")
-PROBE = os.path.join(PKG, "probe_coissue")
 ORACLE_LIB = os.path.join(ORACLE, "liboracle.so")
 
 
@@ -85,11 +83,7 @@ def build(verbose=False):
              os.path.join(CSRC, "runner.cpp"), "-o", objs["runner"]],
             ["gcc", "-O3", "-mavx2", "-ffp-contract=off", "-fopenmp", "-fPIC", "-shared", "-std=c11",
              os.path.join(ORACLE, "fmha_oracle.c"), "-o", ORACLE_LIB + ".tmp", "-lm"],
-            [HIPCC, *HIP_FLAGS, os.path.join(CSRC, "probe_coissue.hip"), "-o", os.path.join(tmp, "probe_coissue")],
         ], verbose)
-        shutil.copyfile(os.path.join(tmp, "probe_coissue"), PROBE + ".tmp")
-        os.chmod(PROBE + ".tmp", 0o755)
-        os.replace(PROBE + ".tmp", PROBE)
         os.replace(ORACLE_LIB + ".tmp", ORACLE_LIB)
         tmp_lib = os.path.join(tmp, "libfmha_native_amd.so")
         _run_all([[HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", objs["kernel"], objs["api"], objs["merge"], objs["runner"],
@@ -107,4 +101,4 @@ def build(verbose=False):
 
 if __name__ == "__main__":
     build(verbose="-v" in sys.argv)
-    print("built", LIB, BENCH, PROBE, ORACLE_LIB)
+    print("built", LIB, BENCH, ORACLE_LIB)

@@ -20,10 +20,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 constexpr int kMaxGridYZ = 65535;  // largest grid y / z dimension
 
 // Largest byte offset touched inside one (batch, head) of a tensor with `rows`
-// rows must fit the 31-bit buffer offsets the kernel uses; the loaders may
-// read up to one 64-key tile past the last row (zero-filled by the bound).
+// rows must fit the 31-bit buffer offsets the kernel uses.  Row indices run
+// past the last row by at most one 64-key tile (K/V loaders) or, for Q and O,
+// by the rest of the block's M-tiles: up to 2*kM0 - 1 rows for the pair form's
+// second M-tile.  Such rows are zero-filled or dropped by the descriptor bound,
+// but their offsets are still computed in 32-bit arithmetic.
 bool offsets_fit(int rows, int stride) {
-    const int64_t max_rows = (int64_t)rows + FMHA_KN0 + FMHA_KM0;
+    const int64_t max_rows = (int64_t)rows + FMHA_KN0 + 2 * FMHA_KM0;
     return max_rows * (int64_t)stride * 2 + 256 < ((int64_t)1 << 31);
 }
 
@@ -36,6 +39,9 @@ extern "C" hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* p, int batch,
     if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o)) return hipErrorInvalidValue;
     if (p->lse != nullptr && (reinterpret_cast<uintptr_t>(p->lse) & 3u)) return hipErrorInvalidValue;
     if (p->seqlen_q < 0 || p->seqlen_k < 0) return hipErrorInvalidValue;
+    // the running max assumes a positive scale (a larger score is a larger
+    // probability); NaN fails this comparison too
+    if (!(p->scale > 0.0f) || p->scale > 3.402823466e38f) return hipErrorInvalidValue;
     if (p->nhead_q <= 0 || p->nhead_k <= 0 || p->nhead_q % p->nhead_k != 0) return hipErrorInvalidValue;
     const int strides[12] = {p->stride_q, p->nhead_stride_q, p->batch_stride_q, p->stride_k, p->nhead_stride_k,
                              p->batch_stride_k, p->stride_v, p->nhead_stride_v, p->batch_stride_v, p->stride_o,
@@ -72,10 +78,6 @@ int device_cus() {
     return n;
 }
 
-#ifndef FMHA_SPLIT_POLICY
-#define FMHA_SPLIT_POLICY 2  // 0: always regular, 1: always split-KV, 2: by grid shape (pick_variant)
-#endif
-
 // Form choice from the grid (measured on MI355X, 256 CUs, all forms on one
 // box; blocks = regular-grid blocks, pairs = pair-grid blocks):
 //  * split-KV (two 4-wave groups per M-tile, one block per CU, each group
@@ -93,8 +95,6 @@ int device_cus() {
 //  * regular: everything else (the dense B4 H16 S2048 and causal B1 H16 S8192
 //    benchmark grids among them).
 int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_t cus) {
-    if (FMHA_SPLIT_POLICY == 0) return FMHA_VARIANT_REGULAR;
-    if (FMHA_SPLIT_POLICY == 1) return FMHA_VARIANT_SPLITKV;
     // blocks (up to ~2^63) is only compared, never multiplied; cus < 2^31
     if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
     if (causal && (blocks <= 3 * cus / 2 || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;

@@ -65,11 +65,13 @@ constexpr int kRowBytes = 128;                 // 64 bf16 per K/V row in LDS
 constexpr int kTileBytes = kTileN * kRowBytes; // 8 KiB
 constexpr int kRing = 4;                       // stages per ring (K and V)
 constexpr int kLoadsPerTile = 2;                   // 1 KiB DMA per load, per wave
-#ifndef FMHA_GROW_SUM
-#define FMHA_GROW_SUM 65536.0f
-#endif
-constexpr float kGrowSum = FMHA_GROW_SUM;          // tile-sum bound of the speculative softmax
-constexpr float kMaxSeed = -5000.0f;               // raw-score running max seed (pipeline.hpp:248-252)
+constexpr float kGrowSum = 65536.0f;               // tile-sum bound of the speculative softmax
+// Running-max seed, in the scaled (exp2) domain: below every finite scaled
+// score, so a row's first visible key always re-frames it (its P overflows
+// the bound).  The reference seeds -5000 raw-score units (pipeline.hpp:248-252),
+// which drops rows whose every score lies below that; its CPU checker
+// (cpu_ref.cpp:124-136) has no seed at all, and neither has this kernel.
+constexpr float kMaxSeed = -3.402823466e38f;       // -FLT_MAX
 constexpr uint32_t kBufferWord3 = 0x00020000u;     // raw dword buffer, gfx9 family
 
 // sched_group_barrier instruction classes
@@ -172,14 +174,8 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 // 12 slots and the last GEMM0 chain runs bare.  A rigid even spread (every
 // slot fenced with sched_barrier, 7 VALU each) gives the same bits and is
 // 2-3% slower on the benchmark grids.
-#ifndef FMHA_VALU_PER_SLOT
-#define FMHA_VALU_PER_SLOT 7
-#endif
-#ifndef FMHA_DS_AHEAD
-#define FMHA_DS_AHEAD 2
-#endif
-constexpr int kValuPerSlot = FMHA_VALU_PER_SLOT;
-constexpr int kDsAhead = FMHA_DS_AHEAD;
+constexpr int kValuPerSlot = 7;
+constexpr int kDsAhead = 2;
 template <bool kG1, bool kG0>
 struct IterSchedule {
     static constexpr int kMfma = 8 * (int(kG1) + int(kG0));
@@ -205,7 +201,7 @@ struct IterSchedule {
 // Online-softmax state of one lane's query row (both lane halves of a row keep
 // the same m_ref; l_part is this lane's partial sum).
 struct Softmax {
-    float m_ref;   // reference max (raw score units)
+    float m_ref;   // reference max, scaled: max of s * scale (exp2 domain)
     float l_part;  // partial row sum of P in the m_ref frame, tiles before the current one
     float l_tile;  // this lane's sum of P over the current tile
 };
@@ -428,10 +424,10 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
                                fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7])));
         return wave_max_halves(mx);
     };
-    // P = exp2(s*scale - m_ref*scale), bf16-packed into the GEMM1 B operands,
+    // P = exp2(s*scale - m_ref), bf16-packed into the GEMM1 B operands,
     // and this lane's tile sum of P (fp32, before the bf16 rounding).
     auto exp_tile = [&](const f32x16* s, bf16x8* pp) {
-        const float neg_ms = -sm.m_ref * scale;
+        const float neg_ms = -sm.m_ref;
         float ls[4];  // 4 independent partial chains (latency)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -470,8 +466,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     auto settle = [&](const f32x16* s, bf16x8* pp) {
         if (__builtin_amdgcn_ballot_w64(!(sm.l_tile <= kGrowSum))) {
             asm volatile("" ::: "memory");  // a side effect: keeps the rare path a branch, not speculated
-            const float m_new = fmaxf(sm.m_ref, tile_max(s));
-            const float alpha = __builtin_amdgcn_exp2f((sm.m_ref - m_new) * scale);
+            const float m_new = fmaxf(sm.m_ref, tile_max(s) * scale);
+            const float alpha = __builtin_amdgcn_exp2f(sm.m_ref - m_new);
             sm.m_ref = m_new;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
@@ -549,9 +545,10 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         gemm0(P0{}, sacc[0]);
         // m_ref starts at the first tile's exact (masked) row max, so the
         // speculative softmax holds from tile 0 on (rows with no visible key
-        // there keep the finite seed: their P is exactly 0)
+        // there keep the finite seed: their P is exactly 0 until a visible
+        // score overflows the bound and re-frames the row)
         mask_tile(0, sacc[0]);
-        sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]));
+        sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]) * scale);
         // iteration 0 has no GEMM1; iterations 1 .. ntg-1 run in groups of
         // kRing (phases 1 2 3 0) and the 0-3 left over, each with GEMM0 of
         // the next tile (for the last one a dead, zero-filled tile)
@@ -606,8 +603,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         if (group == 1) return;
         const float m1 = x[32 * 64 + lane];
         const float m = fmaxf(sm.m_ref, m1);
-        const float a0 = __builtin_amdgcn_exp2f((sm.m_ref - m) * scale);
-        const float a1 = __builtin_amdgcn_exp2f((m1 - m) * scale);
+        const float a0 = __builtin_amdgcn_exp2f(sm.m_ref - m);
+        const float a1 = __builtin_amdgcn_exp2f(m1 - m);
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -617,7 +614,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     }
 
     // ---- epilogue: O = O^T / l (rows < sq; the buffer bound drops the rest),
-    // LSE = (log2(l) + scale*m) * ln2 (natural log, -inf for an empty row) ----
+    // LSE = (log2(l) + m_ref) * ln2 (natural log, -inf for an empty row) ----
     const float l_tot = wave_sum_halves(sm.l_part);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     {
@@ -673,7 +670,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             lse_base = p.lse + (int64_t)h * (p.nhead_stride_q / p.stride_q) + off_q;
         else
             lse_base = p.lse + (int64_t)b * p.nhead_q * p.seqlen_q + (int64_t)h * p.seqlen_q;
-        const float lse2 = __builtin_log2f(l_tot) + sm.m_ref * scale;  // -inf when l == 0
+        const float lse2 = __builtin_log2f(l_tot) + sm.m_ref;  // -inf when l == 0
         lse_base[my_row] = lse2 * 0.69314718055994530942f;
     }
 }

@@ -1,23 +1,31 @@
 """rocprofv3 evidence harness for the FMHA forward kernels (run on the GPU box).
 
-    python -m fmha_native_amd.rocprof --out gpurun_out/prof [--summary profiles/NAME.md]
+    python -m fmha_native_amd.rocprof --out gpurun_out/prof --summary profiles/NAME.md --json profiles/NAME.json
 
 The gfx950 counterpart of the reference's ATT/counter configuration
-(scripts/rocprof_att.yaml:1-17).  It runs ``bench.py`` under ``rocprofv3`` in
-separate passes (a counter pass never combines with tracing, and each pass
-stays within one pass's hardware counter budget), each as a child process
-under its own time limit, and writes a markdown summary with the exact
-command of every pass:
+(scripts/rocprof_att.yaml:1-17).  Everything below runs in one process tree
+on one GPU, so the figures describe one box at one clock.  ``bench.py`` runs
+under ``rocprofv3`` in separate passes (a counter pass never combines with
+tracing, and each pass stays within one pass's hardware counter budget), each
+as a child process under its own time limit; the markdown summary gives the
+exact command of every pass:
 
-1. kernel trace + stats for cfg2 (dense B4 H16 S2048) and cfg3 (causal
-   B1 H16 S8192 + LSE): average dispatch duration, set beside bench.py's own
-   HIP-event time for the same launches;
-2. HBM traffic of cfg2: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by
-   what the counter reads for a device copy of known size (bench.py
-   ``--copy-probe-mib``), against the algorithmic bytes;
-3. utilisation of cfg2 and cfg3: clock (GRBM_GUI_ACTIVE), MFMA busy cycles,
-   VALU/MFMA/LDS instruction counts, LDS bank conflicts, plus the VGPR/AGPR/
-   SGPR/LDS allocation the profiler records for the dispatch.
+0. ``bench.py`` itself, unprofiled: its HIP-event time per launch on cfg2
+   (dense B4 H16 S2048) and cfg3 (causal B1 H16 S8192 + LSE);
+1. kernel trace + stats of cfg2 and cfg3: average dispatch duration, set
+   beside bench.py's own HIP-event time for the same launches;
+2. HBM traffic of cfg2 and cfg3: FETCH_SIZE and WRITE_SIZE per dispatch, each
+   scaled by what the counter reads for a device copy of known size
+   (bench.py ``--copy-probe-mib``), against the algorithmic bytes;
+3. utilisation of cfg2 and cfg3: clock (GRBM_GUI_ACTIVE cycles over the same
+   dispatch's own duration), MFMA busy cycles, VALU/MFMA/LDS instruction
+   counts, LDS bank conflicts, plus the VGPR/AGPR/SGPR/LDS allocation the
+   profiler records for the dispatch.  MFMA busy x clock / 2.4 GHz is the
+   fraction of the 2516.6 TFLOP/s peak those dispatches reach, a check on the
+   HIP-event figure that needs no timer.
+
+The JSON (``--json``) carries the figures ``bench.py`` quotes in its
+``roofline`` object (traffic, MFMA busy, clock) with the run they came from.
 """
 import argparse
 import glob
@@ -70,22 +78,33 @@ def _kernel_stats(db):
 
 
 def _counters(db, kernel_prefix="fmha_fwd"):
-    """Per-dispatch counter values (summed over the chip), averaged over dispatches."""
+    """Per-dispatch counter values (summed over the chip), averaged over the
+    dispatches of each kernel after its first; also the dispatches' own
+    average duration (ns) from the same pass."""
     con = sqlite3.connect(db)
     per = defaultdict(float)
+    dur = {}
     res = {}
     q = ("select dispatch_id, kernel_name, counter_name, value, vgpr_count, accum_vgpr_count, sgpr_count, "
-         "lds_block_size from counters_collection")
-    for disp, kname, cname, val, vgpr, agpr, sgpr, lds in con.execute(q):
+         "lds_block_size, start, end from counters_collection")
+    for disp, kname, cname, val, vgpr, agpr, sgpr, lds, t0, t1 in con.execute(q):
         per[(kname, cname, disp)] += val
+        dur[(kname, disp)] = t1 - t0
         res.setdefault(kname, {"vgpr": vgpr, "agpr": agpr, "sgpr": sgpr, "lds_bytes": lds})
     agg = defaultdict(list)
-    for (k, c, _d), v in per.items():
-        agg[(k, c)].append(v)
+    for (k, c, d), v in per.items():
+        agg[(k, c)].append((d, v))
     out = {}
-    for (k, c), v in agg.items():
+    for (k, c), dv in agg.items():
         if k.startswith(kernel_prefix) or not kernel_prefix:
-            out.setdefault(k, dict(res[k]))[c] = sum(v) / len(v)
+            dv.sort()
+            vals = [v for _, v in (dv[1:] if len(dv) > 1 else dv)]
+            e = out.setdefault(k, dict(res[k]))
+            e[c] = sum(vals) / len(vals)
+            ds = sorted((d, t) for (kk, d), t in dur.items() if kk == k)
+            ds = ds[1:] if len(ds) > 1 else ds
+            e["dispatch_ns"] = sum(t for _, t in ds) / len(ds)
+            e["dispatches"] = len(ds)
     return out
 
 
@@ -93,40 +112,62 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "prof"))
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
-    ap.add_argument("--traffic-json", default=None, help="also write the cfg2 traffic figures here")
+    ap.add_argument("--json", default=None, help="also write the figures bench.py quotes here")
     ap.add_argument("--steps", type=int, default=100)
     args = ap.parse_args()
     os.makedirs(args.out, exist_ok=True)
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on cfg2 (dense B4 H16 S2048) and cfg3 (causal B1 H16 "
           "S8192 + LSE)", "",
-          "MI355X (gfx950), one GPU.  Made by `python -m fmha_native_amd.rocprof`, which runs the passes below "
-          "from the repo root (each under `timeout -s KILL`).", ""]
+          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof` on one box "
+          "(the passes below, from the repo root, each under `timeout -s KILL`).", ""]
+    fig = {"made_by": "python -m fmha_native_amd.rocprof" + (f" --json {os.path.relpath(args.json, ROOT)}"
+                                                             if args.json else "")}
+
+    # 0. bench.py itself, unprofiled
+    cmd = [sys.executable, os.path.join(ROOT, "bench.py"), "--steps", str(args.steps), "--warmup", "20",
+           "--no-cpu-baseline", "--no-extra"]
+    print(f"[rocprof] bench: {' '.join(cmd)}", flush=True)
+    r = subprocess.run(["timeout", "-s", "KILL", "300", *cmd], capture_output=True, text=True)
+    line = json.loads([l for l in r.stdout.splitlines() if l.startswith("{")][-1])
+    bench = {"cfg2": {"ms_per_step": line["ms_per_step"], "tflops": line["value"]},
+             "cfg3": {"ms_per_step": line["also"]["ms_per_step"], "tflops": line["also"]["value"]}}
+    fig["bench"] = {"command": f"python3 bench.py --steps {args.steps} --warmup 20 --no-cpu-baseline --no-extra",
+                    **bench}
+    md += ["## bench.py on this box (HIP events on the launch stream, back-to-back launches)", "",
+           f"    python3 bench.py --steps {args.steps} --warmup 20 --no-cpu-baseline --no-extra", "",
+           "| workload | ms per launch | TFLOP/s | % of 2516.6 |", "|---|---|---|---|"]
+    for wl in ("cfg2", "cfg3"):
+        b = bench[wl]
+        md.append(f"| {wl} | {b['ms_per_step']:.5f} | {b['tflops']:.1f} | {100 * b['tflops'] / PEAK_BF16_TFLOPS:.1f}% |")
+    md.append("")
 
     # 1. kernel trace
-    md += ["## Kernel trace (average dispatch duration vs bench.py's HIP events)", "",
+    md += ["## Kernel trace (average dispatch duration vs bench.py's HIP events in the same process)", "",
            "| workload | kernel | dispatches | rocprofv3 avg | bench.py HIP-event avg | TFLOP/s (trace) | % of 2516.6 |",
            "|---|---|---|---|---|---|---|"]
     cmds = []
     trace = {}
     for wl in ("cfg2", "cfg3"):
         steps = args.steps if wl == "cfg2" else args.steps // 2
-        db, line, cmd = _run(f"trace_{wl}", ["--kernel-trace", "--stats"],
-                             _bench("--only", wl, "--steps", str(steps), "--warmup", "10"), args.out, 300)
+        db, pline, cmd = _run(f"trace_{wl}", ["--kernel-trace", "--stats"],
+                              _bench("--only", wl, "--steps", str(steps), "--warmup", "10"), args.out, 300)
         cmds.append(cmd)
         k = [s for s in _kernel_stats(db) if s["name"].startswith("fmha_fwd")][0]
         tf = WORKLOADS[wl]["flops"] / (k["avg_us"] * 1e-6) / 1e12
-        trace[wl] = {"avg_us": k["avg_us"], "bench_us": line["ms_per_step"] * 1e3, "tflops": tf}
-        md.append(f"| {wl} | `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | {line['ms_per_step'] * 1e3:.2f} us "
+        trace[wl] = {"kernel": k["name"], "avg_us": k["avg_us"], "bench_us": pline["ms_per_step"] * 1e3, "tflops": tf}
+        md.append(f"| {wl} | `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | {pline['ms_per_step'] * 1e3:.2f} us "
                   f"| {tf:.1f} | {100 * tf / PEAK_BF16_TFLOPS:.1f}% |")
     md += ["", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
 
     # 2. traffic
     cmds = []
     vals = {}
-    for name, counter, prog in (("pmc_fetch", "FETCH_SIZE", _bench("--only", "cfg2", "--steps", "5", "--warmup", "1")),
-                                ("pmc_write", "WRITE_SIZE", _bench("--only", "cfg2", "--steps", "5", "--warmup", "1")),
-                                ("pmc_copy_fetch", "FETCH_SIZE", _bench("--copy-probe-mib", "256", "--steps", "5")),
-                                ("pmc_copy_write", "WRITE_SIZE", _bench("--copy-probe-mib", "256", "--steps", "5"))):
+    passes = [("pmc_copy_fetch", "FETCH_SIZE", _bench("--copy-probe-mib", "256", "--steps", "5")),
+              ("pmc_copy_write", "WRITE_SIZE", _bench("--copy-probe-mib", "256", "--steps", "5"))]
+    for wl in ("cfg2", "cfg3"):
+        passes += [(f"pmc_fetch_{wl}", "FETCH_SIZE", _bench("--only", wl, "--steps", "5", "--warmup", "1")),
+                   (f"pmc_write_{wl}", "WRITE_SIZE", _bench("--only", wl, "--steps", "5", "--warmup", "1"))]
+    for name, counter, prog in passes:
         db, _line, cmd = _run(name, ["--pmc", counter], prog, args.out, 120)
         cmds.append(cmd)
         c = _counters(db, kernel_prefix="")
@@ -136,30 +177,37 @@ def main():
             vals[name] = [v[counter] for k, v in c.items() if k.startswith("fmha_fwd")][0]
     copy_kib = 256 * 1024
     fs, ws = copy_kib / vals["pmc_copy_fetch"], copy_kib / vals["pmc_copy_write"]
-    fetch_b = vals["pmc_fetch"] * fs * 1024
-    write_b = vals["pmc_write"] * ws * 1024
-    traffic = fetch_b + write_b
-    alg = WORKLOADS["cfg2"]["bytes"]
-    md += ["## HBM traffic (cfg2, per dispatch)", "",
-           "| counter | kernel (KiB/dispatch) | 256 MiB copy reads (KiB) | scale | scaled bytes |", "|---|---|---|---|---|",
-           f"| FETCH_SIZE | {vals['pmc_fetch']:,.0f} | {vals['pmc_copy_fetch']:,.0f} (expected 262,144) | x{fs:.3f} | "
-           f"{fetch_b / 1e6:.2f} MB |",
-           f"| WRITE_SIZE | {vals['pmc_write']:,.0f} | {vals['pmc_copy_write']:,.0f} (expected 262,144) | x{ws:.3f} | "
-           f"{write_b / 1e6:.2f} MB |", "",
-           f"Total {traffic / 1e6:.2f} MB per launch vs {alg / 1e6:.2f} MB algorithmic (Q+K+V read once, O written "
-           f"once): ratio {traffic / alg:.3f}.", "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
+    md += ["## HBM traffic (per dispatch)", "",
+           f"FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what each reads for a 256 MiB device copy "
+           f"(expected 262,144 KiB each way): FETCH_SIZE read {vals['pmc_copy_fetch']:,.0f} KiB (x{fs:.3f}), "
+           f"WRITE_SIZE {vals['pmc_copy_write']:,.0f} KiB (x{ws:.3f}).", "",
+           "| workload | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) | scaled bytes | algorithmic bytes | ratio |",
+           "|---|---|---|---|---|---|"]
+    traffic = {}
+    for wl in ("cfg2", "cfg3"):
+        t = vals[f"pmc_fetch_{wl}"] * fs * 1024 + vals[f"pmc_write_{wl}"] * ws * 1024
+        alg = WORKLOADS[wl]["bytes"]
+        traffic[wl] = {"fetch_kib": vals[f"pmc_fetch_{wl}"], "write_kib": vals[f"pmc_write_{wl}"],
+                       "hbm_bytes": int(t), "algorithmic_bytes": alg}
+        md.append(f"| {wl} | {vals[f'pmc_fetch_{wl}']:,.0f} | {vals[f'pmc_write_{wl}']:,.0f} | {t / 1e6:.2f} MB | "
+                  f"{alg / 1e6:.2f} MB | {t / alg:.3f} |")
+    md += ["", "Algorithmic bytes: Q+K+V read once, O (and LSE) written once.", "", "Commands:", ""]
+    md += [f"    {c}" for c in cmds] + [""]
 
-    # 3. utilisation
-    md += ["## Utilisation counters (per dispatch, summed over the chip)", ""]
+    # 3. utilisation, with the clock from each dispatch's own duration
+    md += ["## Utilisation counters (per dispatch, summed over the chip)", "",
+           "Clock = GRBM_GUI_ACTIVE / 8 XCDs over the same dispatches' duration in this pass; MFMA busy = "
+           "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over those cycles; MFMA busy x clock / 2.4 GHz = fraction of "
+           "the 2516.6 TFLOP/s peak (2.4 GHz is the clock that figure assumes).", ""]
     cmds = []
     rows = []
     for wl in ("cfg2", "cfg3"):
         db, _line, cmd = _run(f"pmc_util_{wl}", ["--pmc", *UTIL_COUNTERS],
-                              _bench("--only", wl, "--steps", "5", "--warmup", "1"), args.out, 120)
+                              _bench("--only", wl, "--steps", "10", "--warmup", "1"), args.out, 120)
         cmds.append(cmd)
         k, c = list(_counters(db).items())[0]
         cycles_xcd = c["GRBM_GUI_ACTIVE"] / NUM_XCD
-        ghz = cycles_xcd / (trace[wl]["avg_us"] * 1e3)  # cycles per ns
+        ghz = cycles_xcd / c["dispatch_ns"]  # cycles per ns
         mfma_busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMD / cycles_xcd
         iters = c["SQ_INSTS_MFMA"] / 16.0  # 16 MFMA per wave per 64-key tile
         rows.append((wl, k, c, ghz, mfma_busy, iters))
@@ -168,31 +216,48 @@ def main():
     md.append("| VGPR / AGPR / SGPR (rocprofv3 dispatch fields) | "
               + " | ".join(f"{r[2]['vgpr']} / {r[2]['agpr']} / {r[2]['sgpr']}" for r in rows) + " |")
     md.append("| LDS bytes per block | " + " | ".join(f"{r[2]['lds_bytes']}" for r in rows) + " |")
-    md.append("| clock from GRBM_GUI_ACTIVE / 8 XCDs | " + " | ".join(f"{r[3]:.2f} GHz" for r in rows) + " |")
+    md.append("| dispatch duration in this pass | " + " | ".join(f"{r[2]['dispatch_ns'] / 1e3:.2f} us" for r in rows)
+              + " |")
+    md.append("| clock (GRBM_GUI_ACTIVE / 8 / duration) | " + " | ".join(f"{r[3]:.3f} GHz" for r in rows) + " |")
     md.append("| MFMA busy (per SIMD, of kernel cycles) | " + " | ".join(f"{100 * r[4]:.1f}%" for r in rows) + " |")
+    md.append("| MFMA busy x clock / 2.4 GHz (fraction of peak) | "
+              + " | ".join(f"{100 * r[4] * r[3] / 2.4:.1f}%" for r in rows) + " |")
     for name in UTIL_COUNTERS[1:]:
         md.append(f"| {name} | " + " | ".join(f"{r[2].get(name, 0):,.0f}" for r in rows) + " |")
     md.append("| VALU instr per wave per 64-key tile (incl. 16 MFMA) | "
               + " | ".join(f"{r[2]['SQ_INSTS_VALU'] / r[5]:.1f}" for r in rows) + " |")
     md.append("| LDS instr per wave per tile | " + " | ".join(f"{r[2]['SQ_INSTS_LDS'] / r[5]:.1f}" for r in rows) + " |")
-    md += ["", "The compiler reports 248-254 VGPRs used per wave for these entries (`; NumVgprs`, checked with "
-           "`tests/test_codegen.py`), allocated as 256: two waves per SIMD. rocprofv3's VGPR field is consistent "
-           "with the descriptor's granule count read as 4 registers per granule where gfx950 wave64 allocates "
-           "8 (31 + 1 granules: 128 shown, 256 allocated).",
-           "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
+    md += ["", "rocprofv3's VGPR field reads the descriptor's granule count as 4 registers per granule where gfx950 "
+           "wave64 allocates 8 (so 128 shown = 256 allocated: two waves per SIMD); `tests/test_codegen.py` checks "
+           "the compiler's own counts.", "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
+
+    for wl, k, c, ghz, busy, _it in rows:
+        fig[wl] = {
+            "kernel": k,
+            "workload": WORKLOADS[wl]["desc"],
+            "bench_ms_per_step": bench[wl]["ms_per_step"],
+            "bench_tflops": bench[wl]["tflops"],
+            "trace_avg_us": round(trace[wl]["avg_us"], 3),
+            "trace_tflops": round(trace[wl]["tflops"], 2),
+            "trace_bench_us": round(trace[wl]["bench_us"], 3),
+            "counter_dispatch_us": round(c["dispatch_ns"] / 1e3, 3),
+            "clock_ghz": round(ghz, 4),
+            "mfma_busy": round(busy, 4),
+            "frac_from_counters": round(busy * ghz / 2.4, 4),
+            "hbm_bytes_per_launch": traffic[wl]["hbm_bytes"],
+            "algorithmic_bytes": traffic[wl]["algorithmic_bytes"],
+            "fetch_kib_per_dispatch": traffic[wl]["fetch_kib"],
+            "write_kib_per_dispatch": traffic[wl]["write_kib"],
+        }
+    fig["fetch_scale"], fig["write_scale"] = round(fs, 4), round(ws, 4)
 
     path = args.summary or os.path.join(args.out, "summary.md")
     with open(path, "w") as f:
         f.write("\n".join(md))
     print("\n".join(md), flush=True)
-    if args.traffic_json:
-        with open(args.traffic_json, "w") as f:
-            json.dump({"kernel": "fmha_fwd_d64_bf16_msk0", "workload": "cfg2 B4 H16 S2048 D64 dense",
-                       "fetch_kib_per_dispatch": vals["pmc_fetch"], "write_kib_per_dispatch": vals["pmc_write"],
-                       "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
-                       "hbm_bytes_per_launch": int(traffic), "algorithmic_bytes": alg,
-                       "rocprof_avg_us": round(trace["cfg2"]["avg_us"], 3),
-                       "made_by": "python -m fmha_native_amd.rocprof"}, f, indent=1)
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(fig, f, indent=1)
 
 
 if __name__ == "__main__":

@@ -17,6 +17,9 @@
 //
 //   ref_verify -b B -h H [--kv-heads K] -s S [--kv-seq SK] [--mask 0|1]
 //              [--lse 0|1] [--varlen-seqs a,b,...] [--seed N]
+//              [--dump-inputs PATH]   also write h_Q, h_K, h_V as filled by the
+//                                     reference's fill_random (raw uint16, in
+//                                     that order) to PATH
 //   ref_verify --stdin      one case per input line, same flags, one
 //                           REF_VERIFY line per case (one process, one HIP init)
 #include <omp.h>
@@ -43,6 +46,7 @@ static void die(const char* what, hipError_t e) {
 static int run_case(const std::vector<std::string>& args) {
     int b = 1, h = 2, kvh = 0, s = 128, kvs = 0, mask = 0, lse = 0;
     unsigned seed = 42;
+    std::string dump_path;
     std::vector<int> seqs;
     for (size_t i = 0; i < args.size(); ++i) {
         const std::string& a = args[i];
@@ -56,6 +60,7 @@ static int run_case(const std::vector<std::string>& args) {
         else if (a == "--mask") mask = atoi(v);
         else if (a == "--lse") lse = atoi(v);
         else if (a == "--seed") seed = (unsigned)strtoul(v, nullptr, 10);
+        else if (a == "--dump-inputs") dump_path = v;
         else if (a == "--varlen-seqs") {
             for (const char* p = v; *p;) {
                 seqs.push_back(atoi(p));
@@ -84,6 +89,16 @@ static int run_case(const std::vector<std::string>& args) {
 
     FmhaBuffers bufs(p);
     bufs.fill_random(seed);
+    if (!dump_path.empty()) {
+        FILE* f = fopen(dump_path.c_str(), "wb");
+        if (!f) { fprintf(stderr, "ref_verify: cannot write %s\n", dump_path.c_str()); return 2; }
+        const std::vector<uint16_t>* parts[3] = {&bufs.h_Q, &bufs.h_K, &bufs.h_V};
+        for (const auto* a : parts)
+            if (fwrite(a->data(), 2, a->size(), f) != a->size()) { fclose(f); return 2; }
+        fclose(f);
+        printf("REF_INPUTS {\"q\": %zu, \"k\": %zu, \"v\": %zu}\n", bufs.h_Q.size(), bufs.h_K.size(),
+               bufs.h_V.size());
+    }
     bufs.copy_to_device();
 
     float* d_lse_kern = nullptr;

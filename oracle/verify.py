@@ -53,10 +53,14 @@ def baseline_rule(o_ref, o_kern, atol=1e-2, rtol=1e-2):
     ker = np.asarray(o_kern, dtype=np.float32)
     err = np.abs(ref - ker)
     finite = np.isfinite(ker).all()
-    bad = err > atol + rtol * np.abs(ref)
+    tol = atol + rtol * np.abs(ref)
+    bad = err > tol
     return {
         "max_abs": float(np.nanmax(err)) if err.size else 0.0,
         "violations": int(np.count_nonzero(bad)),
+        # largest error among the violating elements and its excess over the tolerance there
+        "max_abs_violating": float(err[bad].max()) if bad.any() else 0.0,
+        "max_excess": float((err - tol)[bad].max()) if bad.any() else 0.0,
         "pass": bool(finite and not bad.any()),
     }
 

@@ -158,6 +158,11 @@ def _mut(**kw):
     (_mut(stride_v=56), 1, 0),               # row shorter than 64 elements
     (_mut(nhead_stride_k=-64), 1, 0),
     (_mut(seqlen_q=-1), 1, 0),
+    (_mut(scale=0.0), 1, 0),                 # the running max needs a positive scale
+    (_mut(scale=-0.18), 1, 0),
+    (_mut(scale=float("nan")), 1, 0),
+    (_mut(scale=float("inf")), 1, 0),
+    (_mut(seqlen_k=16_776_894), 1, 0),       # one row past the 31-bit offset bound (rows + 320 rows of headroom)
     (_mut(nhead_k=3), 1, 0),                 # nhead_q % nhead_k != 0
     (_mut(nhead_k=0), 1, 0),
     (_mut(seqstart_q=0x15000), 1, 0),        # only one seqstart pointer
@@ -170,6 +175,16 @@ def _mut(**kw):
 ])
 def test_check_rejects(params, batch, causal):
     assert fmha.check_params(params, batch, causal) == INVALID
+
+
+def test_offset_bound_edge():
+    """The last row count the 31-bit offset check accepts for 64-element rows:
+    (rows + 64 + 256) * 128 bytes + 256 < 2^31."""
+    assert fmha.check_params(_mut(seqlen_k=16_776_893), 1, 0) == 0
+    assert fmha.check_params(_mut(seqlen_k=16_776_894), 1, 0) == INVALID
+    # Q and O: the same bound with a wider row stride (grid y caps seqlen_q first otherwise)
+    assert fmha.check_params(_mut(seqlen_q=8_388_286, stride_q=128), 1, 0) == 0
+    assert fmha.check_params(_mut(seqlen_q=8_388_287, stride_q=128), 1, 0) == INVALID
 
 
 def test_variant_validation():

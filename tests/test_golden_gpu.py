@@ -40,6 +40,42 @@ def _need_gpu():
     fmha.load_library()
 
 
+@pytest.mark.parametrize("args,geom", [
+    (["-b", "1", "-h", "2", "-s", "128", "--seed", "42"], None),   # cfg1: the golden fixture's inputs
+    (["-b", "2", "-h", "4", "--kv-heads", "2", "-s", "200", "--kv-seq", "333", "--seed", "7"], (2 * 4 * 200, 2 * 2 * 333)),
+    (["-h", "4", "--kv-heads", "1", "--varlen-seqs", "100,257,64", "--seed", "123"], (4 * 421, 1 * 421)),
+])
+def test_reference_fill_random_equals_oracle_generator(tmp_path, args, geom):
+    """The reference's own fill_random (src/runner/buffers.cpp:99-127, compiled
+    into oracle/_ref/ref_verify) writes, bit for bit, the inputs the oracle's
+    generator (oracle_fill_ref) and the product's (fmha.fill_ref) write; for
+    config 1 they also hash to the committed golden digests."""
+    import hashlib
+
+    import oracle
+
+    if not os.path.exists(REF_VERIFY):
+        pytest.skip("oracle/_ref/ref_verify not built (no reference tree where this was built)")
+    path = tmp_path / "inputs.bin"
+    r = subprocess.run([REF_VERIFY, *args, "--dump-inputs", str(path)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    sizes = json.loads([l for l in r.stdout.splitlines() if l.startswith("REF_INPUTS ")][0].split(" ", 1)[1])
+    raw = np.fromfile(path, dtype=np.uint16)
+    nq, nk, nv = sizes["q"], sizes["k"], sizes["v"]
+    assert raw.size == nq + nk + nv
+    ref = raw[:nq], raw[nq:nq + nk], raw[nq + nk:]
+    if geom is not None:
+        assert (nq, nk) == (geom[0] * 64, geom[1] * 64)
+    seed = int(args[args.index("--seed") + 1])
+    for mine in (oracle.fill_ref(seed, nq, nk, nv), fmha.fill_ref(seed, nq, nk, nv)):
+        for a, b in zip(ref, mine):
+            assert np.array_equal(a, b)
+    if geom is None:
+        g = np.load(os.path.join(GOLDEN, "cfg1_ref42.npz"))
+        for name, a in zip("qkv", ref):
+            assert hashlib.sha256(a.tobytes()).hexdigest() == str(g[f"{name}_sha"])
+
+
 def test_kernel_matches_golden_cfg1():
     g = np.load(os.path.join(GOLDEN, "cfg1_ref42.npz"))
     prob = Problem(batch=1, nhead_q=2, seqlen_q=128, lse=True, name="cfg1")

@@ -154,6 +154,9 @@ def _bf16(*shape):
     ("seqstart_dtype", "int32"),
     ("seqstart_k_only", "seqstart_k without"),
     ("cpu", "same GPU"),
+    ("varlen_lse_head_stride", "head stride"),
+    ("stride_wraps", "32-bit int"),
+    ("varlen_head_stride_wraps", "32-bit int"),
 ])
 def test_params_from_tensors_rejects(case, match):
     """Tensors the kernel cannot take are refused before any pointer is used
@@ -184,5 +187,57 @@ def test_params_from_tensors_rejects(case, match):
         kw.update(seqstart_q=ss, seqstart_k=ss, max_seqlen_q=200)
     elif case == "seqstart_k_only":
         kw["seqstart_k"] = torch.tensor([0, 100], dtype=torch.int32)
+    elif case == "varlen_lse_head_stride":
+        # q/o are token slices [4, 300 of 400, 64]: LSE rows of heads >= 1 would land past [4, 300]
+        q, o = _bf16(4, 400, 64)[:, :300], _bf16(4, 400, 64)[:, :300]
+        k, v = _bf16(2, 300, 64), _bf16(2, 300, 64)
+        ss = torch.tensor([0, 100, 300], dtype=torch.int32)
+        kw.update(seqstart_q=ss, seqstart_k=ss, max_seqlen_q=200, lse=torch.zeros((4, 300), dtype=torch.float32))
+    elif case == "stride_wraps":
+        # batch stride 2^32 would read back as 0 from a C int (meta tensors: no memory)
+        big = lambda: torch.empty_strided((2, 256, 262144, 64), (2**32, 2**24, 64, 1), dtype=torch.bfloat16,
+                                          device="meta")
+        q, k, v, o = big(), big(), big(), big()
+    elif case == "varlen_head_stride_wraps":
+        T = 2**25  # head stride T * 64 = 2^31
+        mk = lambda h: torch.empty_strided((h, T, 64), (T * 64, 64, 1), dtype=torch.bfloat16, device="meta")
+        q, k, v, o = mk(2), mk(1), mk(1), mk(2)
+        ss = torch.tensor([0, T], dtype=torch.int32)
+        kw.update(seqstart_q=ss, seqstart_k=ss, max_seqlen_q=T)
     with pytest.raises(ValueError, match=match):
         fmha.params_from_tensors(q, k, v, o, **kw)
+
+
+@pytest.mark.parametrize("case,match", [
+    ("parts_disagree", "must be \\[n"),
+    ("o_dtype", "bfloat16"),
+    ("lse_dtype", "float32"),
+    ("head_dim", "must be \\[n"),
+    ("noncontiguous", "contiguous"),
+    ("o_shape", "o must be"),
+    ("lse_shape", "lse must be"),
+    ("cpu", "same GPU"),
+])
+def test_merge_partials_rejects(case, match):
+    """merge_partials refuses arguments the merge kernel would read or write
+    out of bounds, before any pointer is used."""
+    import torch
+
+    o_parts, lse_parts = _bf16(3, 10, 64), torch.zeros((3, 10), dtype=torch.float32)
+    kw = {}
+    if case == "parts_disagree":
+        lse_parts = torch.zeros((4, 10), dtype=torch.float32)   # 4 LSE parts for 3 O parts
+    elif case == "o_dtype":
+        o_parts = o_parts.float()
+    elif case == "lse_dtype":
+        lse_parts = lse_parts.double()
+    elif case == "head_dim":
+        o_parts = _bf16(3, 10, 32)
+    elif case == "noncontiguous":
+        o_parts = _bf16(3, 20, 64)[:, ::2]
+    elif case == "o_shape":
+        kw["o"] = _bf16(9, 64)
+    elif case == "lse_shape":
+        kw["lse"] = torch.zeros(11, dtype=torch.float32)
+    with pytest.raises(ValueError, match=match):
+        fmha.merge_partials(o_parts, lse_parts, **kw)

@@ -1,7 +1,7 @@
 """GPU tests at the launcher's limits, through the C-ABI.
 
 * the longest key sequence the 31-bit buffer-offset check accepts for 64-wide
-  rows (16,776,000 keys: (rows + 192) * 128 bytes + 256 < 2^31), dense and
+  rows (16,776,000 keys: (rows + 320) * 128 bytes + 256 < 2^31), dense and
   bottom-right causal, in the automatic form and the reference-named entries;
 * the largest grid y: 65,535 M-tiles (seqlen_q = 65,535 * 128);
 * the largest grid z: 65,535 batches, and the tile-major grid with the most
@@ -22,7 +22,7 @@ import fmha_native_amd as fmha
 pytestmark = pytest.mark.gpu
 
 SCALE = 0.125
-MAX_KEYS = 16_776_000  # largest multiple of 1000 below the offset limit (16,777,021 rows)
+MAX_KEYS = 16_776_000  # largest multiple of 1000 below the offset limit (16,776,893 rows)
 
 
 @pytest.fixture(scope="module", autouse=True)

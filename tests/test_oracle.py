@@ -161,6 +161,23 @@ def test_q_zero_uniform_attention():
     assert np.abs(lse - np.log(64)).max() < 1e-6
 
 
+def test_scores_far_below_zero():
+    """Q = 10, K = -10 in every dimension (exact in bf16): every score is -6400
+    raw, -800 after the 1/8 scale.  The softmax is still uniform: O = mean of
+    the visible V rows and LSE = ln(n) - 800 (cpu_ref.cpp:124-136 subtracts the
+    true row max; no fixed seed can drop such a row)."""
+    prob = Problem(batch=1, nhead_q=1, seqlen_q=96, seqlen_k=128, causal=True, lse=True)
+    q, k, v = ref_inputs(prob)
+    q = np.full_like(q, 0x4120)   # bf16 10.0
+    k = np.full_like(k, 0xC120)   # bf16 -10.0
+    o, lse = oracle.run(prob, q, k, v, p_trunc=False)
+    vf = np_ref.bits_to_f64(v).reshape(128, 64)
+    for i in (0, 1, 50, 95):
+        n = i + 32 + 1
+        assert np.abs(o.reshape(96, 64)[i] - vf[:n].mean(0)).max() < 1e-6
+        assert abs(lse[i] - (np.log(n) - 800.0)) < 1e-4  # fp32 LSE near -800: ulp 6e-5
+
+
 def test_single_key():
     """S = 1: P = 1 exactly, O = V0, LSE = q.k / 8."""
     prob = PROBLEMS[-1]
