@@ -27,6 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
+    "VARIANT_PERSISTENT",
     "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
@@ -107,19 +108,21 @@ def load_library(path=LIB_PATH):
     return lib
 
 
-VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR = 0, 1, 2, 3
+VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT = 0, 1, 2, 3, 4
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
-VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR}
+VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
+            "persistent": VARIANT_PERSISTENT}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
     """Launch on ``stream`` (a hipStream_t as int, or None for the null stream).
 
     ``variant``: VARIANT_AUTO (the launcher's choice), VARIANT_REGULAR (the
-    reference-named entries), VARIANT_SPLITKV (the split-KV entries) or
-    VARIANT_PAIR (the pair entries), each optionally OR-ed with
+    reference-named entries), VARIANT_SPLITKV (the split-KV entries),
+    VARIANT_PAIR (the pair entries) or VARIANT_PERSISTENT (dense only: blocks
+    looping over M-tiles), each optionally OR-ed with
     VARIANT_REFERENCE_ORDER (keep the reference's batch-after-batch block order
     for causal dense batches)."""
     lib = load_library()

@@ -10,7 +10,7 @@
 //   --dist ref|normal   reference +-0.1 generator (default) or N(0,1)
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
-//   --variant auto|regular|splitkv|pair   kernel form (default: the launcher's choice)
+//   --variant auto|regular|splitkv|pair|persistent   kernel form (default: the launcher's choice)
 //   --order auto|reference   causal block order (reference: batch after batch)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
@@ -65,7 +65,7 @@ static void usage(const char* prog) {
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
-           "  --variant V      auto|regular|splitkv|pair kernel form [auto]\n"
+           "  --variant V      auto|regular|splitkv|pair|persistent kernel form [auto]\n"
            "  --order O        auto|reference causal block order [auto]\n",
            prog);
 }
@@ -120,7 +120,8 @@ static Config parse(int argc, char** argv) {
                 else if (!strcmp(optarg, "regular")) c.variant = FMHA_VARIANT_REGULAR;
                 else if (!strcmp(optarg, "splitkv")) c.variant = FMHA_VARIANT_SPLITKV;
                 else if (!strcmp(optarg, "pair")) c.variant = FMHA_VARIANT_PAIR;
-                else { fprintf(stderr, "Error: --variant must be auto, regular, splitkv or pair\n"); exit(1); }
+                else if (!strcmp(optarg, "persistent")) c.variant = FMHA_VARIANT_PERSISTENT;
+                else { fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair or persistent\n"); exit(1); }
                 break;
             case 8:
                 if (!strcmp(optarg, "auto")) c.reference_order = false;

@@ -122,6 +122,13 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
  *                         per two adjacent M-tiles of a (batch, head)
+ *   FMHA_VARIANT_PERSISTENT  dense (not varlen) only: one kBlockSize-thread
+ *                         block per resident slot (two per compute unit),
+ *                         each looping over M-tiles taken from per-XCD queues
+ *                         with its K/V pipeline running on from one M-tile
+ *                         into the next; its queue counters live in the
+ *                         library (device memory it owns, no allocation per
+ *                         call; at most 64 such launches in flight per device)
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
@@ -132,6 +139,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
 #define FMHA_VARIANT_PAIR 3
+#define FMHA_VARIANT_PERSISTENT 4
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);

@@ -191,8 +191,8 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    # 0-3 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
-    for bad in (-1, 4, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 4):
+    # 0-4 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
+    for bad in (-1, 5, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 5):
         assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
     bad_p = _mut(q=None)
     assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID

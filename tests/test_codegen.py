@@ -33,10 +33,13 @@ def asm(tmp_path_factory):
 
 
 def _functions(src):
+    """Body of every function symbol (data symbols, such as the persistent
+    form's queue counters, have labels too but no .Lfunc_end)."""
     funcs = {}
-    for m in re.finditer(r"^(_Z[^\s:]+):", src, re.M):
+    for name in re.findall(r"^\s*\.type\s+(_Z[^,\s]+),@function", src, re.M):
+        m = re.search(r"^" + re.escape(name) + r":", src, re.M)
         end = src.index(".Lfunc_end", m.end())
-        funcs[m.group(1)] = src[m.end():end]
+        funcs[name] = src[m.end():end]
     return funcs
 
 
@@ -44,6 +47,8 @@ def test_every_entry_compiled(asm):
     names = _functions(asm)
     for e in _ENTRIES:
         assert any(e + "13FmhaFwdParams" in n for n in names), e
+    for m in (0, 1):
+        assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
 
 
 def test_no_lds_read_in_flight_at_barriers(asm):

@@ -35,14 +35,23 @@ def _report(res):
 
 
 # every kernel form behind the launcher: the reference-named entries, the
-# split-KV entries and the pair entries (the automatic choice is one of them)
-FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR}
+# split-KV entries, the pair entries and the persistent entries (the
+# automatic choice is one of them); the persistent form takes dense problems
+# only (the launcher rejects varlen for it)
+FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR,
+         "persistent": fmha.VARIANT_PERSISTENT}
+
+
+def _dense_only(form, prob):
+    if form == "persistent" and prob.varlen:
+        pytest.skip("the persistent form takes dense problems only")
 
 
 @pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("row", K_ALL_FULL, ids=[r[0] for r in K_ALL_FULL])
 def test_kallfull_matches_oracle(row, form):
     prob = problem_from_row(row)
+    _dense_only(form, prob)
     res = _report(check_problem(prob, dist="ref", seed=42, rule="reference", variant=FORMS[form]))
     assert res["pass"], res
 
@@ -65,6 +74,7 @@ def test_bshd_causal_gqa_smoke():
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
 def test_baseline_configs(cfg, form):
     prob, mult = baseline_problems()[cfg]
+    _dense_only(form, prob)
     res = _report(check_baseline(prob, mult, variant=fmha.VARIANTS[form]))
     # the plain rule against the reference-faithful oracle, recorded for every
     # configuration (cfg5's count and worst case are the contract numbers)
@@ -138,6 +148,8 @@ def test_gqa_equals_replicated_mha_bitwise(form):
 
 @pytest.mark.parametrize("form", list(FORMS))
 def test_varlen_equals_per_sequence_dense_bitwise(form):
+    if form == "persistent":
+        pytest.skip("the persistent form takes dense problems only")
     seqs = (1, 77, 128, 300, 64, 513)
     pv = Problem(batch=0, nhead_q=4, nhead_k=2, seqlen_q=0, causal=True, lse=True, varlen_seqs=seqs)
     q, k, v = make_inputs(pv, "normal", 5)
@@ -209,6 +221,8 @@ def test_masked_and_foreign_keys_contribute_nothing(form):
     wrongly included key would get a sizeable weight; V = 16384.0); the
     row's output bits must not change.  (1) the other sequences of a packed varlen batch, (2) the
     causally masked future key."""
+    if form == "persistent":
+        pytest.skip("the persistent form takes dense problems only")
     seqs = (190, 64, 333)
     T = sum(seqs)
     s0 = seqs[0]
@@ -425,3 +439,80 @@ def test_padded_strides_match_dense(form):
     expect = _pad_bhsd(o_dense, B, H, S, *geo["o"], nan)
     assert np.array_equal(got, expect)  # rows bit-identical, padding untouched
     assert np.array_equal(dl.cpu().numpy(), l_dense)
+
+
+def test_persistent_rejects_varlen():
+    """The persistent form is dense only: a varlen launch asking for it is
+    refused before anything runs."""
+    import torch
+
+    from harness import build_params
+
+    p = Problem(batch=0, nhead_q=2, seqlen_q=0, varlen_seqs=(100, 200))
+    nq, nk, nlse = p.sizes()
+    t = [torch.zeros(n, dtype=torch.int16, device="cuda:0") for n in (nq, nk, nk, nq)]
+    seq = torch.from_numpy(p.seqstart()).to("cuda:0")
+    prm = build_params(p, *t, None, seq)
+    with pytest.raises(fmha.FmhaError):
+        fmha.fmha_fwd_d64_bf16(prm, p.batch, 0, None, fmha.VARIANT_PERSISTENT)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_persistent_queue_state_across_launches(causal):
+    """The persistent form's queue counters are left at zero by every launch:
+    launches of different shapes in a row (many items, fewer items than
+    resident blocks, one item, again many) each give the regular form's bits.
+    A counter left behind would make a later launch skip items (rows left at
+    the sentinel) or run the wrong ones."""
+    shapes = [(4, 16, 16, 2048, 2048), (1, 3, 1, 300, 517), (1, 1, 1, 64, 64), (2, 8, 2, 1500, 1000),
+              (3, 16, 8, 4100, 4100)]
+    for b, h, hk, sq, sk in shapes:
+        p = Problem(batch=b, nhead_q=h, nhead_k=hk, seqlen_q=sq, seqlen_k=sk, causal=causal, lse=True)
+        q, k, v = make_inputs(p, "normal", sq + sk)
+        o_p, l_p = run_kernel(p, q, k, v, variant=fmha.VARIANT_PERSISTENT)
+        o_r, l_r = run_kernel(p, q, k, v, variant=fmha.VARIANT_REGULAR)
+        print("persistent vs regular", (b, h, hk, sq, sk), flush=True)
+        assert np.array_equal(o_p, o_r), (b, h, sq, sk)
+        assert np.array_equal(l_p, l_r), (b, h, sq, sk)
+
+
+def test_persistent_graph_replays_and_concurrent_streams():
+    """Graph capture: every replay (eager work between them) reproduces the
+    eager bits, so the counters a launch leaves behind are what the next
+    replay needs.  Concurrent launches on two streams take different counter
+    slots and give each its own bits."""
+    import torch
+
+    pa = Problem(batch=2, nhead_q=8, nhead_k=4, seqlen_q=2000, seqlen_k=2000, causal=True, lse=True)
+    pb = Problem(batch=4, nhead_q=16, seqlen_q=1024, lse=True)
+    ka, oa, la, prma = _device_problem(pa, 41)
+    kb, ob, lb, prmb = _device_problem(pb, 42)
+    P = fmha.VARIANT_PERSISTENT
+    fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, None, fmha.VARIANT_REGULAR)
+    fmha.fmha_fwd_d64_bf16(prmb, pb.batch, 0, None, fmha.VARIANT_REGULAR)
+    torch.cuda.synchronize()
+    ref_a, ref_la, ref_b, ref_lb = oa.clone(), la.clone(), ob.clone(), lb.clone()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, torch.cuda.current_stream().cuda_stream, P)
+    noise = torch.randn(1 << 20, device="cuda:0")
+    for i in range(4):
+        oa.zero_()
+        la.zero_()
+        noise.mul_(1.0001)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ref_a) and torch.equal(la, ref_la), i
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        oa.zero_()
+        ob.zero_()
+        torch.cuda.synchronize()
+        for _ in range(4):
+            fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, sa.cuda_stream, P)
+            fmha.fmha_fwd_d64_bf16(prmb, pb.batch, 0, sb.cuda_stream, P)
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ref_a) and torch.equal(la, ref_la)
+        assert torch.equal(ob, ref_b) and torch.equal(lb, ref_lb)
