@@ -27,7 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANT_PERSISTENT",
+    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
@@ -90,6 +90,15 @@ def load_library(path=LIB_PATH):
     lib.fmha_fwd_d64_bf16_pick_variant.restype = ctypes.c_int
     lib.fmha_fwd_d64_bf16_tile_major.argtypes = [P, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_tile_major.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_ws.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+    lib.fmha_fwd_d64_bf16_ws.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_workspace_size.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.fmha_fwd_d64_bf16_workspace_size.restype = ctypes.c_int64
+    lib.fmha_fwd_d64_bf16_balanced_plan.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.POINTER(ctypes.c_uint16), ctypes.c_int,
+                                                    ctypes.POINTER(ctypes.c_int)]
+    lib.fmha_fwd_d64_bf16_balanced_plan.restype = ctypes.c_int
     ip = ctypes.POINTER(ctypes.c_int)
     lib.fmha_fwd_d64_bf16_tile_config.argtypes = [ip, ip, ip, ip]
     lib.fmha_fwd_d64_bf16_tile_config.restype = None
@@ -108,12 +117,12 @@ def load_library(path=LIB_PATH):
     return lib
 
 
-VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT = 0, 1, 2, 3, 4
+VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT, VARIANT_BALANCED = 0, 1, 2, 3, 4, 5
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
-            "persistent": VARIANT_PERSISTENT}
+            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
@@ -132,6 +141,44 @@ def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
         rc = lib.fmha_fwd_d64_bf16_variant(ctypes.byref(params), int(batch), int(causal), int(variant), stream)
     if rc != HIP_SUCCESS:
         raise FmhaError(rc)
+
+
+def fmha_fwd_d64_bf16_ws(params, batch, causal, workspace=None, workspace_bytes=0, stream=None,
+                         variant=VARIANT_AUTO):
+    """The launch with a workspace (device pointer as int, 256-byte aligned,
+    at least :func:`workspace_size` bytes; None with 0 bytes allowed), which
+    lets dense causal launches with few heavy M-tiles run the balanced form.
+    ``variant``: VARIANT_AUTO, VARIANT_BALANCED or any other (workspace
+    unused).  Raises :class:`FmhaError` on a non-zero hipError_t."""
+    rc = load_library().fmha_fwd_d64_bf16_ws(ctypes.byref(params), int(batch), int(causal), int(variant), workspace,
+                                             int(workspace_bytes), stream)
+    if rc != HIP_SUCCESS:
+        raise FmhaError(rc, "fmha_fwd_d64_bf16_ws")
+
+
+def workspace_size(params, batch, causal, variant=VARIANT_AUTO):
+    """Workspace bytes :func:`fmha_fwd_d64_bf16_ws` needs (0: none; -1:
+    rejected arguments).  Host only."""
+    return load_library().fmha_fwd_d64_bf16_workspace_size(ctypes.byref(params), int(batch), int(causal),
+                                                           int(variant))
+
+
+def balanced_plan(params, batch, causal, compute_units=0, force=False):
+    """(items, split_from) of the balanced form's plan: items per (batch,
+    head) in dispatch order as (M-tile, half) pairs, half None for a whole
+    M-tile; ([], None) when the launch would not be balanced.  Host only."""
+    cap = 4096
+    buf = (ctypes.c_uint16 * cap)()
+    sf = ctypes.c_int(-1)
+    n = load_library().fmha_fwd_d64_bf16_balanced_plan(ctypes.byref(params), int(batch), int(causal),
+                                                       int(compute_units), int(bool(force)), buf, cap,
+                                                       ctypes.byref(sf))
+    if n < 0:
+        raise FmhaError(HIP_ERROR_INVALID_VALUE, "fmha_fwd_d64_bf16_balanced_plan")
+    if n == 0:
+        return [], None
+    items = [(v & 0x7FFF, (v >> 15) if (v & 0x7FFF) >= sf.value else None) for v in buf[:n]]
+    return items, sf.value
 
 
 def check_params(params, batch, causal):
@@ -297,7 +344,13 @@ def fmha_fwd(q, k, v, causal=False, return_lse=False, seqstart_q=None, seqstart_
     batch = (seqstart_q.numel() - 1) if seqstart_q is not None else q.shape[0]
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
-    fmha_fwd_d64_bf16(p, batch, 1 if causal else 0, stream)
+    causal = 1 if causal else 0
+    need = workspace_size(p, batch, causal)
+    if need > 0:  # the balanced form: a workspace from torch's allocator, freed after this stream's work
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        fmha_fwd_d64_bf16_ws(p, batch, causal, ws.data_ptr(), need, stream)
+    else:
+        fmha_fwd_d64_bf16(p, batch, causal, stream)
     return o, lse
 
 

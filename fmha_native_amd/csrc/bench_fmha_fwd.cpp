@@ -10,7 +10,9 @@
 //   --dist ref|normal   reference +-0.1 generator (default) or N(0,1)
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
-//   --variant auto|regular|splitkv|pair|persistent   kernel form (default: the launcher's choice)
+//   --variant auto|regular|splitkv|pair|persistent|balanced   kernel form (default: the launcher's choice)
+//   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws), so the automatic choice may be
+//                    the balanced causal form; --variant balanced implies it
 //   --order auto|reference   causal block order (reference: batch after batch)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
@@ -45,6 +47,7 @@ struct Config {
     std::string dist = "ref";
     int variant = FMHA_VARIANT_AUTO;
     bool reference_order = false;
+    bool workspace = false;
     float scale_inputs = 1.0f;
     std::vector<int> varlen_seqs;
 };
@@ -65,7 +68,8 @@ static void usage(const char* prog) {
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
-           "  --variant V      auto|regular|splitkv|pair|persistent kernel form [auto]\n"
+           "  --variant V      auto|regular|splitkv|pair|persistent|balanced kernel form [auto]\n"
+           "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [0]\n"
            "  --order O        auto|reference causal block order [auto]\n",
            prog);
 }
@@ -87,6 +91,7 @@ static Config parse(int argc, char** argv) {
                                    {"dist", required_argument, 0, 4},
                                    {"scale-inputs", required_argument, 0, 5},
                                    {"variant", required_argument, 0, 7},
+                                   {"workspace", required_argument, 0, 9},
                                    {"order", required_argument, 0, 8},
                                    {"help", no_argument, 0, 0},
                                    {0, 0, 0, 0}};
@@ -121,13 +126,18 @@ static Config parse(int argc, char** argv) {
                 else if (!strcmp(optarg, "splitkv")) c.variant = FMHA_VARIANT_SPLITKV;
                 else if (!strcmp(optarg, "pair")) c.variant = FMHA_VARIANT_PAIR;
                 else if (!strcmp(optarg, "persistent")) c.variant = FMHA_VARIANT_PERSISTENT;
-                else { fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair or persistent\n"); exit(1); }
+                else if (!strcmp(optarg, "balanced")) c.variant = FMHA_VARIANT_BALANCED;
+                else {
+                    fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair, persistent or balanced\n");
+                    exit(1);
+                }
                 break;
             case 8:
                 if (!strcmp(optarg, "auto")) c.reference_order = false;
                 else if (!strcmp(optarg, "reference")) c.reference_order = true;
                 else { fprintf(stderr, "Error: --order must be auto or reference\n"); exit(1); }
                 break;
+            case 9: c.workspace = atoi(optarg) != 0; break;
             case 0: usage(argv[0]); exit(0);
             default: usage(argv[0]); exit(1);
         }
@@ -215,10 +225,21 @@ int main(int argc, char** argv) {
         p.batch_stride_k = p.batch_stride_v = c.kv_heads * c.kv_seq_len * D;
     }
 
+    const int variant = c.variant | (c.reference_order ? FMHA_VARIANT_REFERENCE_ORDER : 0);
+    void* dws = nullptr;
+    int64_t ws_bytes = 0;
+    const bool use_ws = c.workspace || c.variant == FMHA_VARIANT_BALANCED;
+    if (use_ws) {
+        ws_bytes = fmha_fwd_d64_bf16_workspace_size(&p, c.batch, c.mask, variant);
+        if (ws_bytes < 0) {
+            fprintf(stderr, "fmha_fwd_d64_bf16_workspace_size rejected the arguments\n");
+            exit(1);
+        }
+        if (ws_bytes > 0) HIP_CHECK(hipMalloc(&dws, (size_t)ws_bytes));
+    }
     auto launch = [&]() {
-        hipError_t e = fmha_fwd_d64_bf16_variant(&p, c.batch, c.mask,
-                                                c.variant | (c.reference_order ? FMHA_VARIANT_REFERENCE_ORDER : 0),
-                                                nullptr);
+        hipError_t e = use_ws ? fmha_fwd_d64_bf16_ws(&p, c.batch, c.mask, variant, dws, ws_bytes, nullptr)
+                              : fmha_fwd_d64_bf16_variant(&p, c.batch, c.mask, variant, nullptr);
         if (e != hipSuccess) {
             fprintf(stderr, "fmha_fwd_d64_bf16 failed: %d (%s)\n", (int)e, hipGetErrorString(e));
             exit(1);
@@ -268,5 +289,6 @@ int main(int argc, char** argv) {
     (void)hipFree(dout);
     if (dlse) (void)hipFree(dlse);
     if (dseq) (void)hipFree(dseq);
+    if (dws) (void)hipFree(dws);
     return 0;
 }

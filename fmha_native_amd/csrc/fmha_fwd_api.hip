@@ -9,7 +9,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
+#include <vector>
 
 #include "fmha_fwd.h"
 #include "fmha_internal.h"
@@ -130,6 +132,123 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
 }
 
 }  // namespace
+
+namespace {
+
+// Key tiles of causal M-tile mt (pipeline.hpp:168-193, as the kernel).
+int causal_ntiles(const FmhaFwdParams* p, int mt) {
+    const int sq = p->seqlen_q, sk = p->seqlen_k;
+    const int last = std::min(mt * kM0 + kM0 - 1, sq - 1);
+    const int e = last + (sk - sq) + 1;
+    const int kv_end = e < 0 ? 0 : (e > sk ? sk : e);
+    return (kv_end + kN0 - 1) / kN0;
+}
+
+// Plan of a balanced causal launch on `cus` compute units (two resident
+// blocks each): the M-tiles whose key tiles exceed half the average work per
+// resident block are split into two key halves (so none outlasts the average
+// much), and the items are ordered by work, heaviest first (longest
+// processing time first; ties: later M-tile, first half).  Without `force`
+// the plan is taken only when the heaviest M-tile exceeds the average work
+// per resident block (otherwise the regular heaviest-first order balances
+// already).  Returns false when there is no plan (not causal dense, too many
+// items for the table); fills `a` (table, split range) when given.
+bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force, FmhaBalancedArgs* a,
+                   int64_t* ws_bytes) {
+    if (!causal || p->seqstart_q != nullptr || batch <= 0 || p->seqlen_q <= 0 || cus <= 0) return false;
+    const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
+    if (m_tiles > FMHA_BALANCED_MAX_ITEMS) return false;
+    double total = 0.0;
+    for (int mt = 0; mt < m_tiles; ++mt) total += causal_ntiles(p, mt);
+    total *= (double)p->nhead_q * batch;
+    const double avg = total / (2.0 * (double)cus);  // key tiles per resident block
+    const int heaviest = causal_ntiles(p, m_tiles - 1);
+    if (!force && heaviest <= avg) return false;
+    const double limit = std::max(2.0, avg / 2);
+    int split_from = m_tiles;  // key tiles grow with the M-tile: the split ones are a suffix
+    while (split_from > 0 && causal_ntiles(p, split_from - 1) > limit) --split_from;
+    const int n_split = m_tiles - split_from;
+    const int n_items = split_from + 2 * n_split;
+    if (n_items > FMHA_BALANCED_MAX_ITEMS) return false;
+    if (ws_bytes) *ws_bytes = (int64_t)n_split * p->nhead_q * batch * 2 * FMHA_BALANCED_PART_BYTES;
+    if (a) {
+        struct It {
+            int w, mt, half;
+        };
+        std::vector<It> items;
+        items.reserve(n_items);
+        for (int mt = 0; mt < m_tiles; ++mt) {
+            const int n = causal_ntiles(p, mt);
+            if (mt < split_from) {
+                items.push_back({n, mt, 0});
+            } else {
+                items.push_back({(n + 1) / 2, mt, 0});
+                items.push_back({n / 2, mt, 1});
+            }
+        }
+        std::stable_sort(items.begin(), items.end(), [](const It& x, const It& y) {
+            if (x.w != y.w) return x.w > y.w;
+            if (x.mt != y.mt) return x.mt > y.mt;
+            return x.half < y.half;
+        });
+        for (int i = 0; i < n_items; ++i) a->item[i] = (unsigned short)(items[i].mt | (items[i].half << 15));
+        a->split_from = split_from;
+        a->n_split = n_split;
+        a->n_items = n_items;
+        a->pad = 0;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* p, int batch, int causal, int compute_units,
+                                               int force, unsigned short* items, int capacity, int* split_from) {
+    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
+    FmhaBalancedArgs a;
+    if (!balanced_plan(p, batch, causal, compute_units > 0 ? compute_units : device_cus(), force != 0, &a, nullptr))
+        return 0;
+    if (items != nullptr)
+        for (int i = 0; i < a.n_items && i < capacity; ++i) items[i] = a.item[i];
+    if (split_from != nullptr) *split_from = a.split_from;
+    return a.n_items;
+}
+
+extern "C" int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* p, int batch, int causal, int variant) {
+    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
+    const int v = variant & ~FMHA_VARIANT_REFERENCE_ORDER;
+    if (v != FMHA_VARIANT_AUTO && v != FMHA_VARIANT_BALANCED) return 0;
+    int64_t bytes = 0;
+    if (!balanced_plan(p, batch, causal, device_cus(), v == FMHA_VARIANT_BALANCED, nullptr, &bytes)) return 0;
+    return bytes;
+}
+
+extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, int causal, int variant,
+                                           void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
+    if (chk != hipSuccess) return chk;
+    const int v = variant & ~FMHA_VARIANT_REFERENCE_ORDER;
+    if (v != FMHA_VARIANT_AUTO && v != FMHA_VARIANT_BALANCED)
+        return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
+    if (workspace_bytes < 0 || (workspace == nullptr && workspace_bytes != 0) ||
+        (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return hipErrorInvalidValue;
+    if (batch == 0 || p->seqlen_q == 0) return hipSuccess;
+    FmhaBalancedArgs a;
+    int64_t need = 0;
+    const bool plan = balanced_plan(p, batch, causal, device_cus(), v == FMHA_VARIANT_BALANCED, &a, &need);
+    if (v == FMHA_VARIANT_BALANCED && (!plan || need > workspace_bytes)) return hipErrorInvalidValue;
+    if (!plan || need > workspace_bytes) return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
+    a.p = *p;
+    a.part = (float*)workspace;
+    hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_msk1, dim3(p->nhead_q, batch, a.n_items), dim3(kBlockSize), 0,
+                       stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.n_split == 0) return e;
+    hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_merge, dim3(p->nhead_q, a.n_split, batch), dim3(kBlockSize), 0,
+                       stream, a);
+    return hipGetLastError();
+}
 
 extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch, int causal, int compute_units) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;

@@ -75,6 +75,7 @@ constexpr float kGrowSum = 65536.0f;               // tile-sum bound of the spec
 // (cpu_ref.cpp:124-136) has no seed at all, and neither has this kernel.
 constexpr float kMaxSeed = -3.402823466e38f;       // -FLT_MAX
 constexpr uint32_t kBufferWord3 = 0x00020000u;     // raw dword buffer, gfx9 family
+constexpr int kPartFloatsPerWave = 34 * 64;        // balanced form: one wave's partial result (O^T, m, l)
 
 // sched_group_barrier instruction classes
 constexpr int kSchedVALU = 0x002;
@@ -221,10 +222,20 @@ struct Softmax {
 //    The shared barrier keeps both in lockstep: two separate blocks on one
 //    compute unit progress unevenly (one is served first), so the CU's last
 //    block runs alone at the end; a pair has no such tail.
-enum : int { kModeRegular = 0, kModeSplitKV = 1, kModePair = 2 };
+//  * kModeBalanced: one group, one item of a balanced causal launch: the
+//    whole M-tile, or one half of its key tiles (a split M-tile), whose
+//    partial result goes to a workspace slot for the merge launch.
+enum : int { kModeRegular = 0, kModeSplitKV = 1, kModePair = 2, kModeBalanced = 3 };
+// The key range of a balanced-launch item: `part` null for a whole M-tile;
+// otherwise half `half` of its key tiles and the slot of its partial result.
+struct Chunk {
+    int half;
+    float* part;
+};
 template <bool kCausal, bool kVarlen, int kMode>
-__device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, const Ring& ring) {
-    constexpr int kGroups = kMode == kModeRegular ? 1 : 2;
+__device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, int mt, const Ring& ring,
+                                          Chunk ck = Chunk{0, nullptr}) {
+    constexpr int kGroups = (kMode == kModeRegular || kMode == kModeBalanced) ? 1 : 2;
     constexpr bool kSplitKV = kMode == kModeSplitKV;
     constexpr bool kPair = kMode == kModePair;
     constexpr int kLoads = kPair ? 1 : kLoadsPerTile;  // DMA loads per wave, tensor and tile
@@ -289,8 +300,15 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     const int ntiles = (kv_end + kTileN - 1) / kTileN;
     // this group's key tiles: global tiles [tile0, tile0 + ntg) (the loops
     // below count group-local tiles 0 .. ntg-1); tiles >= tile_end are dead
-    const int ntg = kSplitKV ? (ntiles + 1) / 2 : ntiles;
-    const int tile0 = kSplitKV ? group * ntg : 0;
+    int ntg = kSplitKV ? (ntiles + 1) / 2 : ntiles;
+    int tile0 = kSplitKV ? group * ntg : 0;
+    if constexpr (kMode == kModeBalanced) {
+        if (ck.part != nullptr) {  // a split M-tile: the first ceil(n/2) key tiles, or the rest
+            const int h0 = (ntiles + 1) / 2;
+            tile0 = ck.half ? h0 : 0;
+            ntg = ck.half ? ntiles - h0 : h0;
+        }
+    }
     const int tile_end = min(ntiles, tile0 + ntg);
 
     const int wrow0 = row0 + wave * kRowsPerWave;  // first query row of this wave
@@ -613,6 +631,23 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             for (int r = 0; r < 16; ++r) oacc[db][r] = a0 * oacc[db][r] + a1 * x[(16 * db + r) * 64 + lane];
         sm.l_part = a0 * sm.l_part + a1 * x[33 * 64 + lane];
         sm.m_ref = m;
+    }
+
+    if constexpr (kMode == kModeBalanced) {
+        // a split M-tile's half: its unnormalised O^T, reference max and partial
+        // row sums, lane-major (element e of lane L of wave w at
+        // part[(34w + e) * 64 + L]: every store writes 256 contiguous bytes);
+        // the merge launch finishes the M-tile
+        if (ck.part != nullptr) {
+            float* w = ck.part + wave * kPartFloatsPerWave;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) w[(16 * db + r) * 64 + lane] = oacc[db][r];
+            w[32 * 64 + lane] = sm.m_ref;
+            w[33 * 64 + lane] = sm.l_part;
+            return;
+        }
     }
 
     // ---- epilogue: O = O^T / l (rows < sq; the buffer bound drops the rest),
@@ -1356,4 +1391,87 @@ extern "C" int* fmha_persist_queue_slot(unsigned slot) {
         base[dev].store(b, std::memory_order_release);
     }
     return b + (size_t)(slot % kQueueSlots) * (kQueues + 1) * kQueueStride;
+}
+
+// ---- balanced causal entries (this build's own; no counterpart in the
+// reference): dense causal launches whose heaviest M-tiles outlast the average
+// work per resident block.  Grid (nhead_q, batch, n_items); item z of every
+// (batch, head) comes from the launcher's table, heaviest first: a whole
+// M-tile, or one half of the key tiles of a split M-tile, whose partial result
+// goes to the workspace; fmha_fwd_d64_bf16_balanced_merge then finishes the
+// split M-tiles. ----
+static_assert(FMHA_BALANCED_PART_BYTES == kWaves * kPartFloatsPerWave * 4, "partial slot size");
+__device__ __forceinline__ Chunk balanced_chunk(const FmhaBalancedArgs& a, int b, int h, int mt, int half) {
+    if (mt < a.split_from) return Chunk{0, nullptr};
+    const int64_t slot = ((int64_t)(b * a.p.nhead_q + h) * a.n_split + (mt - a.split_from)) * 2 + half;
+    return Chunk{half, a.part + slot * (kWaves * kPartFloatsPerWave)};
+}
+FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_balanced_msk1(FmhaBalancedArgs args) {
+    FMHA_RING(ring, kTileBytes)
+    const int it = args.item[blockIdx.z];
+    const int mt = it & 0x7fff, half = it >> 15;
+    const int b = blockIdx.y, h = blockIdx.x;
+    fwd_mtile<true, false, kModeBalanced>(args.p, b, h, mt, ring, balanced_chunk(args, b, h, mt, half));
+}
+
+// Merge of the two halves of a split M-tile (grid (nhead_q, n_split, batch)):
+// thread (wave, lane) holds the same O^T elements in both partials, so each
+// lane merges its own: m = max(m0, m1), O^T = sum 2^(m_i - m) O^T_i, l alike;
+// then the regular epilogue (O = O^T / l through LDS, LSE).
+__global__ __launch_bounds__(FMHA_KBLOCK) void fmha_fwd_d64_bf16_balanced_merge(FmhaBalancedArgs args) {
+    __shared__ __attribute__((aligned(1024))) char stage[kWaves * kRowsPerWave * kRowBytes];
+    const FmhaFwdParams& p = args.p;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int mt = args.split_from + blockIdx.y, h = blockIdx.x, b = blockIdx.z;
+    const float* w0 = balanced_chunk(args, b, h, mt, 0).part + wave * kPartFloatsPerWave;
+    const float* w1 = w0 + kWaves * kPartFloatsPerWave;
+    const float m0 = w0[32 * 64 + lane], m1 = w1[32 * 64 + lane];
+    const float m = fmaxf(m0, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m0 - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
+    f32x16 oacc[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            oacc[db][r] = a0 * w0[(16 * db + r) * 64 + lane] + a1 * w1[(16 * db + r) * 64 + lane];
+    const float l_part = a0 * w0[33 * 64 + lane] + a1 * w1[33 * 64 + lane];
+
+    const float l_tot = wave_sum_halves(l_part);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int sq = p.seqlen_q;
+    const uint32_t obytes = (uint32_t)((int64_t)(sq - 1) * p.stride_o * 2 + kRowBytes);
+    const auto ro = make_rsrc((const __bf16*)p.o + (int64_t)b * p.batch_stride_o + (int64_t)h * p.nhead_stride_o, obytes);
+    const int wrow0 = mt * kTileM + wave * kRowsPerWave;
+    lds_char* tb = (lds_char*)stage + wave * (kRowsPerWave * kRowBytes);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            bf16x2 x0, x1;
+            x0[0] = (__bf16)(oacc[db][4 * g4 + 0] * inv);
+            x0[1] = (__bf16)(oacc[db][4 * g4 + 1] * inv);
+            x1[0] = (__bf16)(oacc[db][4 * g4 + 2] * inv);
+            x1[1] = (__bf16)(oacc[db][4 * g4 + 3] * inv);
+            i32x2 v;
+            v[0] = __builtin_bit_cast(int, x0);
+            v[1] = __builtin_bit_cast(int, x1);
+            const int c = 4 * db + g4;
+            *(lds_i32x2*)(tb + l32 * kRowBytes + ((c ^ ((l32 >> 1) & 7)) << 4) + 8 * (hi ^ (l32 & 1))) = v;
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 8; ++i) {
+        const int r = 8 * i + (lane >> 3), pc = lane & 7;
+        const i32x4 raw = *(const lds_i32x4*)(tb + r * kRowBytes + (pc << 4));
+        const i32x4 v = (r & 1) ? i32x4{raw[2], raw[3], raw[0], raw[1]} : raw;
+        const int c = pc ^ ((r >> 1) & 7);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * p.stride_o * 2 + c * 16, 0, 0);
+    }
+    const int my_row = wrow0 + l32;
+    if (p.lse != nullptr && hi == 0 && my_row < sq) {
+        const float lse2 = __builtin_log2f(l_tot) + m;  // -inf when l == 0
+        p.lse[(int64_t)b * p.nhead_q * sq + (int64_t)h * sq + my_row] = lse2 * 0.69314718055994530942f;
+    }
 }

@@ -140,9 +140,50 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_SPLITKV 2
 #define FMHA_VARIANT_PAIR 3
 #define FMHA_VARIANT_PERSISTENT 4
+#define FMHA_VARIANT_BALANCED 5 /* fmha_fwd_d64_bf16_ws only: it needs a workspace */
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
+
+/* The launch with a caller-provided workspace (this build's own; no
+ * counterpart in the reference).  Dense causal launches whose heaviest M-tile
+ * would outlast the average work per resident block (long sequences with few
+ * heads, e.g. B1 H2 S40000) run the balanced form: the M-tiles with more key
+ * tiles than half that average are split into two key halves, every item is
+ * dispatched heaviest first from a table in the kernarg, each half leaves its
+ * partial result in the workspace and a second launch merges the halves
+ * (fp32, the same merge as the split-KV form; results equal the other forms
+ * up to fp32 rounding order).
+ *   variant: FMHA_VARIANT_AUTO (balanced when it applies and the workspace
+ *            is large enough, else what fmha_fwd_d64_bf16 picks),
+ *            FMHA_VARIANT_BALANCED (always the balanced form, with the
+ *            heavy-M-tile rule applied even where the regular order would
+ *            balance: causal dense only; hipErrorInvalidValue if it cannot
+ *            run), or any other variant (workspace unused, as
+ *            fmha_fwd_d64_bf16_variant).
+ *   workspace: device memory, 256-byte aligned, at least
+ *            fmha_fwd_d64_bf16_workspace_size() bytes, or NULL with 0 bytes
+ *            (then never balanced).  Its contents need no initialisation;
+ *            launches that overlap in time need workspaces of their own.
+ * Allocates nothing.  Returns hipSuccess, hipErrorInvalidValue (nothing
+ * launched) or the launch error. */
+hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* params, int batch, int causal, int variant, void* workspace,
+                                int64_t workspace_bytes, hipStream_t stream);
+/* Workspace bytes fmha_fwd_d64_bf16_ws needs for these arguments with
+ * FMHA_VARIANT_AUTO or FMHA_VARIANT_BALANCED on the current device (0 when the
+ * launch would not use one; 0 for any other variant), -1 for rejected
+ * arguments.  Host only. */
+int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* params, int batch, int causal, int variant);
+
+/* The balanced form's plan for these arguments on a device with
+ * `compute_units` compute units (0 = the current device's; `force` as
+ * FMHA_VARIANT_BALANCED): writes up to `capacity` items (dispatch order;
+ * M-tile | half << 15, half 0 = the first ceil(n/2) key tiles) and the first
+ * split M-tile, and returns the number of items per (batch, head); 0 when
+ * the launch would not be balanced, -1 for rejected arguments.  Host only
+ * (this build's own; no counterpart in the reference). */
+int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* params, int batch, int causal, int compute_units, int force,
+                                    unsigned short* items, int capacity, int* split_from);
 
 /* Argument checks of fmha_fwd_d64_bf16 without launching (host only, no GPU
  * needed).  Returns hipSuccess or hipErrorInvalidValue. */

@@ -71,7 +71,13 @@ def run_kernel(prob, q, k, v, stream=None, variant=0):
     p = build_params(prob, dq, dk, dv, do, dlse, dseq)
     if stream is None:
         stream = torch.cuda.current_stream().cuda_stream
-    fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), stream, variant)
+    if variant == fmha.VARIANT_BALANCED:
+        # the balanced form runs through the workspace entry point
+        need = fmha.workspace_size(p, prob.batch, int(prob.causal), variant)
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda:0")
+        fmha.fmha_fwd_d64_bf16_ws(p, prob.batch, int(prob.causal), ws.data_ptr(), need, stream, variant)
+    else:
+        fmha.fmha_fwd_d64_bf16(p, prob.batch, int(prob.causal), stream, variant)
     torch.cuda.synchronize()
     o = do.cpu().numpy().view(np.uint16)
     lse = dlse.cpu().numpy() if dlse is not None else None

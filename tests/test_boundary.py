@@ -300,3 +300,71 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+# ---------------------------------------------------------------- balanced causal form (host only)
+
+def _ntiles(mt, sq, sk):
+    last = min(mt * 128 + 127, sq - 1)
+    e = max(0, min(sk, last + (sk - sq) + 1))
+    return (e + 63) // 64
+
+
+@pytest.mark.parametrize("b,h,sq,sk,cus,force", [
+    (1, 2, 40000, 40000, 256, False),   # cfg5: heavy M-tiles
+    (1, 2, 40000, 40000, 304, False),
+    (2, 3, 3000, 3500, 256, True),
+    (1, 1, 300, 200, 256, True),
+])
+def test_balanced_plan_is_longest_first_over_every_key_tile(b, h, sq, sk, cus, force):
+    """The plan covers every key tile of every M-tile exactly once (whole
+    M-tiles below split_from, two halves from it on), in non-increasing order
+    of work, and splits exactly the M-tiles with more key tiles than half the
+    average work per resident block (two blocks per compute unit)."""
+    p = valid_params(lse=False)
+    p.nhead_q, p.nhead_k, p.seqlen_q, p.seqlen_k = h, h, sq, sk
+    items, sf = fmha.balanced_plan(p, b, 1, cus, force)
+    m_tiles = -(-sq // 128)
+    n = [_ntiles(mt, sq, sk) for mt in range(m_tiles)]
+    avg = sum(n) * h * b / (2 * cus)
+    assert sf == sum(1 for x in n if x <= max(2.0, avg / 2))
+    expect = {(mt, None) for mt in range(sf)} | {(mt, half) for mt in range(sf, m_tiles) for half in (0, 1)}
+    assert len(items) == len(expect) and set(items) == expect
+    work = [n[mt] if half is None else (n[mt] + 1) // 2 if half == 0 else n[mt] // 2 for mt, half in items]
+    assert all(x >= y for x, y in zip(work, work[1:]))
+    ws = fmha.workspace_size(p, b, 1, fmha.VARIANT_BALANCED if force else fmha.VARIANT_AUTO) if cus == 256 else None
+    if ws is not None:
+        assert ws == (m_tiles - sf) * h * b * 2 * 4 * 34 * 64 * 4
+
+
+@pytest.mark.parametrize("b,h,sq,causal", [(4, 16, 2048, 0), (4, 16, 2048, 1), (1, 16, 8192, 1), (1, 4, 32768, 1)])
+def test_balanced_plan_only_where_the_heaviest_m_tile_outlasts_the_average(b, h, sq, causal):
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = h
+    p.seqlen_q = p.seqlen_k = sq
+    assert fmha.balanced_plan(p, b, causal, 256) == ([], None)
+    assert fmha.workspace_size(p, b, causal) == 0
+
+
+def test_ws_entry_rejects_bad_workspaces_and_forms():
+    """Refused before anything is launched (no GPU needed)."""
+    lib = fmha.load_library()
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = 2
+    p.seqlen_q = p.seqlen_k = 40000
+    B = fmha.VARIANT_BALANCED
+    need = fmha.workspace_size(p, 1, 1, B)
+    assert need > 0
+    ws = 1 << 20
+    for args in [(1, 1, B, ws + 8, need),          # not 256-byte aligned
+                 (1, 1, B, ws, need - 1),          # too small for the forced plan
+                 (1, 1, B, None, 5),               # bytes without memory
+                 (1, 1, B, ws, -1),
+                 (1, 0, B, ws, need),              # not causal
+                 (1, 1, 99, ws, need)]:            # unknown form
+        assert lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), *args, None) == INVALID, args
+    assert fmha.workspace_size(_mut(q=None), 1, 1) == -1
+    assert fmha.workspace_size(p, 1, 1, fmha.VARIANT_REGULAR) == 0
+    pv = valid_params(varlen=True, lse=False)      # varlen: never balanced
+    assert lib.fmha_fwd_d64_bf16_ws(ctypes.byref(pv), 1, 1, B, ws, need, None) == INVALID
+    assert fmha.balanced_plan(pv, 1, 1, 256, True) == ([], None)

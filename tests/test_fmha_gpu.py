@@ -40,19 +40,24 @@ def _report(res):
 # only (the launcher rejects varlen for it)
 FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR,
          "persistent": fmha.VARIANT_PERSISTENT}
+# the balanced form (causal dense, through the workspace entry) runs on the
+# matrices of reference cases and benchmark configurations
+MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED)
 
 
 def _dense_only(form, prob):
     if form == "persistent" and prob.varlen:
         pytest.skip("the persistent form takes dense problems only")
+    if form == "balanced" and (prob.varlen or not prob.causal):
+        pytest.skip("the balanced form takes causal dense problems only")
 
 
-@pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("form", list(MATRIX_FORMS))
 @pytest.mark.parametrize("row", K_ALL_FULL, ids=[r[0] for r in K_ALL_FULL])
 def test_kallfull_matches_oracle(row, form):
     prob = problem_from_row(row)
     _dense_only(form, prob)
-    res = _report(check_problem(prob, dist="ref", seed=42, rule="reference", variant=FORMS[form]))
+    res = _report(check_problem(prob, dist="ref", seed=42, rule="reference", variant=MATRIX_FORMS[form]))
     assert res["pass"], res
 
 
@@ -70,7 +75,7 @@ def test_bshd_causal_gqa_smoke():
     assert res["pass"], res
 
 
-@pytest.mark.parametrize("form", ["auto"] + list(FORMS))
+@pytest.mark.parametrize("form", ["auto"] + list(MATRIX_FORMS))
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
 def test_baseline_configs(cfg, form):
     prob, mult = baseline_problems()[cfg]
