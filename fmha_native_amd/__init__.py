@@ -93,6 +93,8 @@ def load_library(path=LIB_PATH):
     lib.fmha_fwd_d64_bf16_ws.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                          ctypes.c_void_p]
     lib.fmha_fwd_d64_bf16_ws.restype = ctypes.c_int
+    lib.fmha_fwd_d64_bf16_noalloc.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.fmha_fwd_d64_bf16_noalloc.restype = ctypes.c_int
     lib.fmha_fwd_d64_bf16_workspace_size.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_workspace_size.restype = ctypes.c_int64
     lib.fmha_fwd_d64_bf16_balanced_plan.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,

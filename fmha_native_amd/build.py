@@ -73,12 +73,14 @@ def build(verbose=False):
             "kernel": os.path.join(tmp, "fmha_fwd_kernel.o"),
             "api": os.path.join(tmp, "fmha_fwd_api.o"),
             "merge": os.path.join(tmp, "fmha_merge.o"),
+            "noalloc": os.path.join(tmp, "fmha_noalloc.o"),
             "runner": os.path.join(tmp, "runner.o"),
         }
         _run_all([
             [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "fmha_fwd_kernel.hip"), "-o", objs["kernel"]],
             [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "fmha_fwd_api.hip"), "-o", objs["api"]],
             [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "fmha_merge.hip"), "-o", objs["merge"]],
+            [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "fmha_noalloc.hip"), "-o", objs["noalloc"]],
             ["g++", "-O3", "-fopenmp", "-fPIC", "-std=c++17", f"-I{CSRC}", "-c",
              os.path.join(CSRC, "runner.cpp"), "-o", objs["runner"]],
             ["gcc", "-O3", "-mavx2", "-ffp-contract=off", "-fopenmp", "-fPIC", "-shared", "-std=c11",
@@ -86,7 +88,7 @@ def build(verbose=False):
         ], verbose)
         os.replace(ORACLE_LIB + ".tmp", ORACLE_LIB)
         tmp_lib = os.path.join(tmp, "libfmha_native_amd.so")
-        _run_all([[HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", objs["kernel"], objs["api"], objs["merge"], objs["runner"],
+        _run_all([[HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", objs["kernel"], objs["api"], objs["merge"], objs["noalloc"], objs["runner"],
                    "-lgomp", "-o", tmp_lib]], verbose)
         shutil.copyfile(tmp_lib, LIB + ".tmp")
         os.replace(LIB + ".tmp", LIB)

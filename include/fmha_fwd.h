@@ -175,6 +175,19 @@ hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* params, int batch, int caus
  * arguments.  Host only. */
 int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* params, int batch, int causal, int variant);
 
+/* fmha_fwd_d64_bf16_ws without a workspace argument, for callers that cannot
+ * allocate (code under graph capture, serving loops that forbid allocation).
+ * No counterpart in the reference.  The workspace is a static device array of
+ * FMHA_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends; a launch whose plan needs more returns
+ * hipErrorInvalidValue and launches nothing (the balanced form needs
+ * 2 x 34,816 bytes per split M-tile: B1 H2 S40000 causal needs 30,359,552).
+ * Calls that overlap in time on one GPU share the array and race; calls in
+ * stream order do not (nothing in it needs clearing).  Allocates nothing. */
+#define FMHA_NOALLOC_SCRATCH_BYTES (32 << 20)
+hipError_t fmha_fwd_d64_bf16_noalloc(const FmhaFwdParams* params, int batch, int causal, int variant,
+                                     hipStream_t stream);
+
 /* The balanced form's plan for these arguments on a device with
  * `compute_units` compute units (0 = the current device's; `force` as
  * FMHA_VARIANT_BALANCED): writes up to `capacity` items (dispatch order;

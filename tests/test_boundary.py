@@ -41,6 +41,7 @@ def header_c_functions():
         text = open(os.path.join(INCLUDE, fn)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"^\s*#.*$", "", text, flags=re.M)  # preprocessor lines (macro values in parentheses)
         text = re.sub(r"typedef struct.*?\}\s*\w+\s*;", "", text, flags=re.S)
         for block in re.findall(r'extern "C" \{(.*?)\n\}', text, flags=re.S):
             names += re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", block)

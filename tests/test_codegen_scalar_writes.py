@@ -15,7 +15,7 @@ import pytest
 
 from fmha_native_amd import build
 
-_SOURCES = ["fmha_fwd_kernel.hip", "fmha_merge.hip", "fmha_fwd_api.hip"]
+_SOURCES = ["fmha_fwd_kernel.hip", "fmha_merge.hip", "fmha_fwd_api.hip", "fmha_noalloc.hip"]
 _FORBIDDEN = re.compile(r"^\s*(s_store_|s_buffer_store|s_scratch_store|s_atomic|s_buffer_atomic|"
                         r"s_dcache_wb|s_dcache_discard)", re.M)
 
