@@ -10,8 +10,11 @@ configuration is reported under ``also``.  A step is one launch of the
 forward over the whole batch with Q/K/V already resident in HBM (through
 fmha_fwd_d64_bf16_ws with a workspace allocated before timing, so the
 launcher's automatic choice may take the balanced causal form: then a step is
-its two launches), timed with the reference's protocol (HIP events around each
-launch); the back-to-back average of as many launches is reported beside it.  Inputs are synthetic
+its two launches), timed back to back between two HIP events on the launch
+stream with synchronisations before and after, once 0.1 s of untimed
+launches has brought the clock up from idle and the W warm-up steps have run;
+the reference's per-launch event protocol is reported beside it
+(``reference_protocol``).  Inputs are synthetic
 N(0,1) bf16 (seed 42).
 
 ``roofline`` carries this run's achieved TFLOP/s and, from the committed
@@ -118,12 +121,32 @@ class _HipEvents:
             self.lib.hipEventDestroy(e)
 
 
-def time_problem(prob, steps, warmup, torch, mult=1.0):
-    """Warm up, then time exactly `steps` launches with the reference's
-    protocol (src/bench_fmha_fwd.cpp:204-210): HIP events recorded on the
-    launch stream right before and after each launch, synchronised per
-    launch, times averaged.  Then the same number of launches back to back
-    between two events (launch gaps hidden), reported beside it."""
+RAMP_SECONDS = 0.1
+
+
+def clock_ramp(launch, torch, seconds=RAMP_SECONDS):
+    """Untimed launches for `seconds` of wall time before the warm-up steps.
+    From an idle GPU the first ~25 ms of back-to-back cfg2 launches run up to
+    2x slower while the clock ramps (MI355X, chunks of 20 launches: 179, 96,
+    91, 84, 80 ... 77.3 us per launch after ~300 launches), so a short warm-up
+    would put the ramp into the timed steps.  Returns the launch count."""
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            assert launch() == 0
+        n += 20
+        torch.cuda.synchronize()
+    return n
+
+
+def time_problem(prob, steps, warmup, torch, mult=1.0, variant=0):
+    """Ramp the clock (clock_ramp), run `warmup` launches, then time exactly
+    `steps` launches back to back on the launch stream between two HIP
+    events, bracketed by synchronisations (the whole-job throughput).  Then the reference's own protocol
+    (src/bench_fmha_fwd.cpp:204-210) over as many launches: events right
+    before and after each launch, synchronised per launch, averaged; it adds
+    the host's launch latency to every step and is reported beside it."""
     import ctypes
 
     import fmha_native_amd as fmha
@@ -135,42 +158,46 @@ def time_problem(prob, steps, warmup, torch, mult=1.0):
     lib = fmha.load_library()
     pp, batch, causal = ctypes.byref(p), prob.batch, int(prob.causal)
     # the launcher with a workspace (allocated before timing): the automatic
-    # choice, which takes the balanced causal form where it applies
-    need = fmha.workspace_size(p, batch, causal)
+    # choice (variant 0), which takes the balanced causal form where it
+    # applies, or the form a profiling run asks for
+    need = fmha.workspace_size(p, batch, causal, variant)
+    assert need >= 0, f"variant {variant} rejected for {prob.name}"
     ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda:0")
     wsp, wsn = ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(need)
 
-    def launch(pp_, b_, c_, s_):
-        return lib.fmha_fwd_d64_bf16_ws(pp_, b_, c_, 0, wsp, wsn, s_)
+    def launch():
+        return lib.fmha_fwd_d64_bf16_ws(pp, batch, causal, variant, wsp, wsn, sh)
 
     hip = _HipEvents()
+    ramp = clock_ramp(launch, torch)
     for _ in range(warmup):
-        assert launch(pp, batch, causal, sh) == 0
-    torch.cuda.synchronize()
+        assert launch() == 0
     e0, e1 = hip.create(2)
-    times = []
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
+    hip.lib.hipEventRecord(e0, sh)
+    for _ in range(steps):
+        launch()
+    hip.lib.hipEventRecord(e1, sh)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = hip.elapsed_ms(e0, e1) / steps
+    times = []
     for _ in range(steps):
         hip.lib.hipEventRecord(e0, sh)
-        rc = launch(pp, batch, causal, sh)
+        rc = launch()
         hip.lib.hipEventRecord(e1, sh)
         hip.lib.hipEventSynchronize(e1)
         assert rc == 0, f"launch returned {rc}"
         times.append(hip.elapsed_ms(e0, e1))
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = sum(times) / steps
-    hip.lib.hipEventRecord(e0, sh)
-    for _ in range(steps):
-        launch(pp, batch, causal, sh)
-    hip.lib.hipEventRecord(e1, sh)
-    torch.cuda.synchronize()
-    b2b = hip.elapsed_ms(e0, e1) / steps
+    ref_ms = sum(times) / steps
     hip.destroy([e0, e1])
+    picked = variant or fmha.pick_variant(p, batch, causal)
     form = "balanced (two launches: items, then the merge of split M-tiles)" if need > 0 else \
-        {1: "regular", 2: "splitkv", 3: "pair"}.get(fmha.pick_variant(p, batch, causal), "?")
-    return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12,
-            "b2b_ms": b2b, "b2b_tflops": prob.flops() / (b2b * 1e-3) / 1e12, "host": host, "form": form,
+        {v: k for k, v in fmha.VARIANTS.items()}.get(picked, "?")
+    return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "ramp": ramp,
+            "ref_ms": ref_ms, "ref_tflops": prob.flops() / (ref_ms * 1e-3) / 1e12, "host": host, "form": form,
             "workspace_bytes": need}
 
 
@@ -188,18 +215,23 @@ def _host_threads():
     return nproc, omp, threads
 
 
-def cpu_baseline_reference(prob):
+def cpu_baseline_reference(prob, heads=None):
     """The reference's own CPU path, cpu_ref_verify (src/runner/cpu_ref.cpp:14-311,
-    compiled from its sources into oracle/_ref/ref_verify), over the whole
-    workload, timed by the harness around that one call.  Its loop nest
-    (cpu_ref.cpp:73-84) is OpenMP over (batch, head) rows and computes every
-    (query, key) score, masked ones included, so a causal problem costs it the
-    dense work.  None if not built."""
+    compiled from its sources into oracle/_ref/ref_verify), timed by the
+    harness around that one call.  Its loop nest (cpu_ref.cpp:73-84) is
+    OpenMP over (batch, head) rows and computes every (query, key) score,
+    masked ones included, so a causal problem costs it the dense work.
+    ``heads``: run that many of the workload's heads (same batch and
+    sequence) and scale the time to all of them; used where the whole
+    workload would take minutes and the sample keeps the loop's parallelism
+    (B*H units handed out 16 at a time: both fit one chunk, one thread).
+    None if not built."""
     import subprocess
 
     if not os.path.exists(REF_VERIFY) or prob.varlen:
         return None
-    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(prob.nhead_q), "-s", str(prob.seqlen_q), "--seed", "42",
+    nh = heads or prob.nhead_q
+    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(nh), "-s", str(prob.seqlen_q), "--seed", "42",
            "--mask", str(int(prob.causal)), "--lse", str(int(prob.lse))]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
@@ -207,28 +239,34 @@ def cpu_baseline_reference(prob):
     res = [json.loads(l.split(" ", 1)[1]) for l in r.stdout.splitlines() if l.startswith("REF_VERIFY ")]
     if not res:
         return None
-    t, thr = res[0]["cpu_ref_seconds"], res[0]["threads"]
+    t_run, thr = res[0]["cpu_ref_seconds"], res[0]["threads"]
     nproc, omp, _ = _host_threads()
     units = prob.batch * prob.nhead_q
     # collapse(2) schedule(dynamic, 16) hands out the B*H (batch, head) units
     # 16 at a time: ceil(B*H / 16) chunks, so at most that many threads work
     chunks = -(-units // 16)
+    if heads:
+        assert -(-(prob.batch * nh) // 16) == chunks == 1, "a head sample must keep the loop's parallelism"
+    t = t_run * prob.nhead_q / nh
     lse = f", LSE |d| max {res[0]['lse_max_abs']:.2e}" if prob.lse else ""
+    shape = f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''}"
+    what = (f"over {nh} of the {prob.nhead_q} heads of the {shape} workload ({t_run:.2f} s, scaled x{prob.nhead_q}/{nh}"
+            f" to {t:.2f} s: one thread computes every head either way, the B*H units all fitting one chunk of 16)"
+            if heads else f"over the full {shape} workload, {t:.2f} s")
     return {
         "value": prob.flops() / t / 1e12,
         "unit": "TFLOP/s",
         "cores": thr,
         "kind": "reference",
         "seconds": round(t, 3),
+        "seconds_measured": round(t_run, 3),
         "nproc": nproc,
         "omp_num_threads": omp,
         "effective_parallelism": min(thr, chunks),
-        "sample": f"the reference's cpu_ref_verify over the full B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}"
-                  f"{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''} workload (its fill_random(42) "
-                  f"inputs; time does not depend on values), {t:.2f} s on {thr} OpenMP threads, of which "
-                  f"min({thr}, ceil(B*H/16) = {chunks}) = {min(thr, chunks)} have work (its loop is collapse(2) "
-                  f"schedule(dynamic, 16) over the B*H = {units} (batch, head) units, cpu_ref.cpp:73-84); FLOPs "
-                  f"by the repo convention"
+        "sample": f"the reference's cpu_ref_verify {what} (its fill_random(42) inputs; time does not depend on "
+                  f"values), on {thr} OpenMP threads, of which min({thr}, ceil(B*H/16) = {chunks}) = "
+                  f"{min(thr, chunks)} have work (its loop is collapse(2) schedule(dynamic, 16) over the "
+                  f"B*H = {units} (batch, head) units, cpu_ref.cpp:73-84); FLOPs by the repo convention"
                   f"{' (x0.5; the loop computes every masked score too)' if prob.causal else ''}; its check of "
                   f"this kernel's output: pass={res[0]['pass']}{lse}",
     }
@@ -312,7 +350,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
-    ap.add_argument("--only", choices=["cfg2", "cfg3"], help="time one workload only (profiling runs)")
+    ap.add_argument("--only", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
+                    help="time one workload only (profiling runs)")
+    ap.add_argument("--variant", default="auto", help="with --only: the kernel form (default: the launcher's choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run `steps` device-to-device copies of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -339,10 +379,12 @@ def main():
         return
     cfg2, cfg3 = _problems()
     if args.only:
-        prob = cfg2 if args.only == "cfg2" else cfg3
-        r = time_problem(prob, args.steps, args.warmup, torch)
-        print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"],
-                          "back_to_back_ms": r["b2b_ms"]}), flush=True)
+        from fmha_native_amd.problem import baseline_problems
+
+        prob, mult = {"cfg2": (cfg2, 1.0), "cfg3": (cfg3, 1.0)}.get(args.only) or baseline_problems()[args.only]
+        r = time_problem(prob, args.steps, args.warmup, torch, mult, fmha.VARIANTS[args.variant])
+        print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"], "form": r["form"],
+                          "reference_protocol_ms": r["ref_ms"]}), flush=True)
         return
     r2 = time_problem(cfg2, args.steps, args.warmup, torch)
     r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)
@@ -356,7 +398,7 @@ def main():
             r = time_problem(prob, max(1, args.steps // 4), max(1, args.warmup // 2), torch, mult)
             e = {"workload": prob.name, "ms_per_step": round(r["ms"], 5), "value": round(r["tflops"], 2),
                  "pct_bf16_peak": round(100.0 * r["tflops"] / PEAK_BF16_TFLOPS, 2),
-                 "back_to_back": {"ms_per_step": round(r["b2b_ms"], 5), "value": round(r["b2b_tflops"], 2)},
+                 "reference_protocol": {"ms_per_step": round(r["ref_ms"], 5), "value": round(r["ref_tflops"], 2)},
                  "form": r["form"]}
             if prob.varlen:
                 e["value_exact_flops"] = round(prob.exact_flops() / (r["ms"] * 1e-3) / 1e12, 2)
@@ -370,9 +412,10 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_reference(cfg2) or cpu_baseline(cfg2, r2["host"])
-        c3 = cpu_baseline_reference(cfg3) or cpu_baseline(cfg3, r3["host"])
+        # the whole of cfg3 takes its loop ~80 s on one thread: 4 of its 16 heads
+        c3 = cpu_baseline_reference(cfg3, heads=4) or cpu_baseline(cfg3, r3["host"])
         cpu["cfg3"] = {k: c3[k] for k in ("value", "unit", "cores", "kind", "seconds", "effective_parallelism",
-                                          "sample")}
+                                          "sample") if k in c3}
 
     achieved = r2["tflops"]
     line = {
@@ -389,9 +432,12 @@ def main():
         "vs_baseline_note": "ratio to the reference's published MI300X figure for this config (348.4 TFLOP/s, "
                             "README.md:91); no MI355X figure is published",
         "pct_bf16_peak": round(100.0 * achieved / PEAK_BF16_TFLOPS, 2),
-        "timing": "per launch, HIP events around each launch on its stream (src/bench_fmha_fwd.cpp:204-210), "
-                  "averaged over the timed steps",
-        "back_to_back": {"ms_per_step": round(r2["b2b_ms"], 5), "value": round(r2["b2b_tflops"], 2)},
+        "timing": "steps launched back to back on one stream between two HIP events, synchronised before and "
+                  "after (whole-job throughput), after 0.1 s of untimed launches that bring the clock up from "
+                  "idle and the warmup steps; reference_protocol: the reference's events around each launch, "
+                  "synchronised per launch (src/bench_fmha_fwd.cpp:204-210), which adds the host's launch latency",
+        "clock_ramp_launches": r2["ramp"],
+        "reference_protocol": {"ms_per_step": round(r2["ref_ms"], 5), "value": round(r2["ref_tflops"], 2)},
         "form": r2["form"],
         "dtype": "bf16",
         "data": "synthetic: Q/K/V i.i.d. N(0,1) bf16, seed 42 (fill_normal)",
@@ -403,7 +449,7 @@ def main():
             "ms_per_step": round(r3["ms"], 5),
             "value": round(r3["tflops"], 2),
             "pct_bf16_peak": round(100.0 * r3["tflops"] / PEAK_BF16_TFLOPS, 2),
-            "back_to_back": {"ms_per_step": round(r3["b2b_ms"], 5), "value": round(r3["b2b_tflops"], 2)},
+            "reference_protocol": {"ms_per_step": round(r3["ref_ms"], 5), "value": round(r3["ref_tflops"], 2)},
             "form": r3["form"],
             "roofline": _roofline(r3["tflops"], "cfg3"),
             "vs_reference_mi300x": round(r3["tflops"] / 358.1, 3),

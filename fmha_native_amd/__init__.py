@@ -27,7 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
+    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "VARIANT_SHORT", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
@@ -120,11 +120,12 @@ def load_library(path=LIB_PATH):
 
 
 VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT, VARIANT_BALANCED = 0, 1, 2, 3, 4, 5
+VARIANT_SHORT = 6
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
-            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED}
+            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):

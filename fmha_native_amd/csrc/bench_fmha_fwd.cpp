@@ -10,7 +10,7 @@
 //   --dist ref|normal   reference +-0.1 generator (default) or N(0,1)
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
-//   --variant auto|regular|splitkv|pair|persistent|balanced   kernel form (default: the launcher's choice)
+//   --variant auto|regular|splitkv|pair|persistent|balanced|short   kernel form (default: the launcher's choice)
 //   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws), so the automatic choice may be
 //                    the balanced causal form; --variant balanced implies it
 //   --order auto|reference   causal block order (reference: batch after batch)
@@ -68,7 +68,7 @@ static void usage(const char* prog) {
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
-           "  --variant V      auto|regular|splitkv|pair|persistent|balanced kernel form [auto]\n"
+           "  --variant V      auto|regular|splitkv|pair|persistent|balanced|short form [auto]\n"
            "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [0]\n"
            "  --order O        auto|reference causal block order [auto]\n",
            prog);
@@ -127,8 +127,9 @@ static Config parse(int argc, char** argv) {
                 else if (!strcmp(optarg, "pair")) c.variant = FMHA_VARIANT_PAIR;
                 else if (!strcmp(optarg, "persistent")) c.variant = FMHA_VARIANT_PERSISTENT;
                 else if (!strcmp(optarg, "balanced")) c.variant = FMHA_VARIANT_BALANCED;
+                else if (!strcmp(optarg, "short")) c.variant = FMHA_VARIANT_SHORT;
                 else {
-                    fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair, persistent or balanced\n");
+                    fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair, persistent, balanced or short\n");
                     exit(1);
                 }
                 break;

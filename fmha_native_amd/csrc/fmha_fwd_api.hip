@@ -84,11 +84,14 @@ int device_cus() {
 // Form choice from the grid (measured on MI355X, 256 CUs, all forms on one
 // box; blocks = regular-grid blocks, pairs = pair-grid blocks):
 //  * split-KV (two 4-wave groups per M-tile, one block per CU, each group
-//    walking half of the keys): when the regular grid cannot fill the GPU —
-//    blocks <= CUs (+8-10% at 128-256 blocks), and for causal grids, whose
-//    heaviest M-tile is the critical path, below 1.5 blocks per CU (+16% at
-//    384 = 1.5 per CU) or up to 2 per CU with long M-tiles (seqlen_k >= 8192:
-//    +6% at 512).  Elsewhere it loses 2-17% to the regular form.
+//    walking half of the keys): when the regular grid cannot fill the GPU and
+//    the M-tiles are long (seqlen_k >= 2048) — blocks <= CUs (+8-14% at
+//    64-256 blocks with 4096 keys), and for causal grids, whose heaviest
+//    M-tile is the critical path, below 1.5 blocks per CU (+16% at 384 = 1.5
+//    per CU) or up to 2 per CU with seqlen_k >= 8192 (+6% at 512).  Elsewhere
+//    it loses 2-17% to the regular form; with few key tiles the halves are
+//    too short to pay for the merge (1024 keys: -2 to +1%; <= 512 keys: -4
+//    to -20%, down to the two-block grid B1 H2 S128).
 //  * pair (two adjacent M-tiles per 8-wave block, one block per CU): the two
 //    blocks a CU holds in the regular form progress unevenly, so each CU's
 //    last block runs alone; a pair block has no such tail, but pays a barrier
@@ -99,8 +102,10 @@ int device_cus() {
 //    benchmark grids among them).
 int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_t cus) {
     // blocks (up to ~2^63) is only compared, never multiplied; cus < 2^31
-    if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
-    if (causal && (blocks <= 3 * cus / 2 || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
+    if (seqlen_k >= 2048) {
+        if (blocks <= cus) return FMHA_VARIANT_SPLITKV;
+        if (causal && (blocks <= 3 * cus / 2 || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
+    }
     const bool whole_rounds = pairs >= cus && pairs % cus == 0;
     if (whole_rounds && seqlen_k >= (causal ? 32768 : 8192)) return FMHA_VARIANT_PAIR;
     return FMHA_VARIANT_REGULAR;
@@ -123,12 +128,28 @@ bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
+// Keys the short form holds at once (two 64-key tiles).
+constexpr int kShortKeys = 2 * FMHA_KN0;
+
 // blocks of the regular grid and of the pair grid
 int64_t grid_blocks(const FmhaFwdParams* p, int batch) {
     return (int64_t)p->nhead_q * ((p->seqlen_q + kM0 - 1) / kM0) * batch;
 }
 int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
     return (int64_t)p->nhead_q * (((p->seqlen_q + kM0 - 1) / kM0 + 1) / 2) * batch;
+}
+
+// The automatic form of a dense launch: the short form when all keys fit two
+// tiles (seqlen_k is exact there) and the launch has at least two blocks'
+// worth of query rows per compute unit, else the grid-shape rule above.
+// Kernel trace, H16, S64 and S128, B1-B128 (dense and causal): the short form
+// is 9-30 % faster from 65,536 rows up (B32 S128, B64 S64) and up to 13 %
+// slower on smaller grids, where one block's latency sets the launch time
+// (B32 S64, 32,768 rows in 512 half-filled blocks: -3.5 %).
+int pick_dense(const FmhaFwdParams* p, int batch, int causal, int64_t cus) {
+    const int64_t rows = (int64_t)batch * p->nhead_q * p->seqlen_q;
+    if (p->seqlen_k <= kShortKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
+    return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
 }
 
 }  // namespace
@@ -252,8 +273,9 @@ extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, in
 
 extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch, int causal, int compute_units) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
-    return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k,
-                        compute_units > 0 ? compute_units : device_cus());
+    const int64_t cus = compute_units > 0 ? compute_units : device_cus();
+    if (p->seqstart_q != nullptr) return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
+    return pick_dense(p, batch, causal, cus);
 }
 
 extern "C" int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* p, int batch, int causal) {
@@ -268,9 +290,11 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     if (chk != hipSuccess) return chk;
     const bool tile_major = (variant & FMHA_VARIANT_REFERENCE_ORDER) == 0 && use_tilemajor(p, batch, causal);
     variant &= ~FMHA_VARIANT_REFERENCE_ORDER;
-    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_PERSISTENT) return hipErrorInvalidValue;
+    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_BALANCED)
+        return hipErrorInvalidValue;  // the balanced form needs fmha_fwd_d64_bf16_ws
     const bool varlen = p->seqstart_q != nullptr;
     if (variant == FMHA_VARIANT_PERSISTENT && varlen) return hipErrorInvalidValue;  // dense only
+    if (variant == FMHA_VARIANT_SHORT && p->seqlen_k > kShortKeys) return hipErrorInvalidValue;
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
@@ -295,7 +319,23 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
         return hipGetLastError();
     }
     if (variant == FMHA_VARIANT_AUTO)
-        variant = pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus());
+        variant = varlen ? pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus())
+                         : pick_dense(p, batch, causal, device_cus());
+    if (variant == FMHA_VARIANT_SHORT) {
+        const dim3 block(kBlockSize);
+        if (varlen) {
+            if (causal)
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk1_varlen, grid, block, 0, stream, *p);
+            else
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk0_varlen, grid, block, 0, stream, *p);
+        } else {
+            if (causal)
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk1, grid, block, 0, stream, *p);
+            else
+                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk0, grid, block, 0, stream, *p);
+        }
+        return hipGetLastError();
+    }
     if (tile_major) {  // causal, dense, batch > 1
         if (variant == FMHA_VARIANT_PAIR)
             hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_msk1_tilemajor, dim3(p->nhead_q, batch, (m_tiles + 1) / 2),

@@ -26,6 +26,23 @@ exact command of every pass:
 
 The JSON (``--json``) carries the figures ``bench.py`` quotes in its
 ``roofline`` object (traffic, MFMA busy, clock) with the run they came from.
+
+    python -m fmha_native_amd.rocprof --forms cfg4:auto,cfg5:auto,cfg5:regular --summary profiles/NAME.md
+
+profiles other workloads in the kernel forms named (``auto`` = the
+launcher's choice; a form the launcher did not pick, beside it, shows what
+the choice gains): per workload and form, ``bench.py --only`` unprofiled, a
+kernel trace of every kernel of a step (the balanced causal form is two: its
+items, then the merge of its split M-tiles) and the utilisation counters of
+each kernel, with the clock from the same dispatches.
+
+    python -m fmha_native_amd.rocprof --short --summary profiles/NAME.md
+
+profiles the short-sequence shapes (262,144 query rows, H16, S 64-512,
+dense and causal) through the bench_fmha_fwd CLI in the launcher's choice
+and in the regular form, cfg1 (kernel-trace duration beside the CLI's
+per-call time), and device copies of the same byte count (the HBM rate a
+plain stream reaches at this size).
 """
 import argparse
 import glob
@@ -108,14 +125,204 @@ def _counters(db, kernel_prefix="fmha_fwd"):
     return out
 
 
+def _util_row(c):
+    """clock (GHz), MFMA busy fraction, fraction of the bf16 peak."""
+    cycles_xcd = c["GRBM_GUI_ACTIVE"] / NUM_XCD
+    ghz = cycles_xcd / c["dispatch_ns"]
+    busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMD / cycles_xcd
+    return ghz, busy, busy * ghz / 2.4
+
+
+def profile_forms(args):
+    """Kernel trace and utilisation counters of other workloads in the forms
+    ``args.forms`` names ("cfg4:auto,cfg5:regular", ...)."""
+    from fmha_native_amd.problem import baseline_problems
+
+    probs = baseline_problems()
+    md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on " + ", ".join(args.forms.split(",")), "",
+          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof --forms "
+          f"{args.forms}` on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
+          "`auto` is the launcher's own choice. TFLOP/s use the repo FLOP convention "
+          "(4·B·H·Sq·Sk·64, ×0.5 causal; varlen counts max(S) for every sequence, and the exact count of "
+          "visible (q, k) pairs is given beside it).", ""]
+    fig = {"made_by": f"python -m fmha_native_amd.rocprof --forms {args.forms}", "forms": {}}
+    for spec in args.forms.split(","):
+        wl, form = spec.split(":")
+        prob, _mult = probs[wl]
+        tag = f"{wl}_{form}"
+        steps = str(args.steps // 4 if wl != "cfg1" else args.steps)
+        # unprofiled
+        cmd = _bench("--only", wl, "--variant", form, "--steps", steps, "--warmup", "5")
+        print(f"[rocprof] bench: {' '.join(cmd)}", flush=True)
+        r = subprocess.run(["timeout", "-s", "KILL", "300", *cmd], capture_output=True, text=True)
+        line = json.loads([l for l in r.stdout.splitlines() if l.startswith("{")][-1])
+        # kernel trace
+        db, tline, tcmd = _run(f"trace_{tag}", ["--kernel-trace", "--stats"],
+                               _bench("--only", wl, "--variant", form, "--steps", steps, "--warmup", "5"),
+                               args.out, 300)
+        ks = [k for k in _kernel_stats(db) if k["name"].startswith("fmha_fwd")]
+        step_us = sum(k["avg_us"] for k in ks)
+        # counters
+        udb, _l, ucmd = _run(f"pmc_util_{tag}", ["--pmc", *UTIL_COUNTERS],
+                             _bench("--only", wl, "--variant", form, "--steps", "5", "--warmup", "1"), args.out, 120)
+        cs = _counters(udb)
+        flops = prob.flops()
+        md += [f"## {wl} ({prob.name}), form `{form}` → {line['form']}", "",
+               f"bench.py (back-to-back HIP events): {line['ms_per_step'] * 1e3:.2f} us per step, "
+               f"{line['tflops']:.1f} TFLOP/s ({100 * line['tflops'] / PEAK_BF16_TFLOPS:.1f}% of 2516.6)"
+               + (f"; exact-count {prob.exact_flops() / (line['ms_per_step'] * 1e-3) / 1e12:.1f} TFLOP/s"
+                  if prob.varlen else "") + ".", "",
+               "| kernel | dispatches | trace avg | clock | MFMA busy | MFMA busy × clock / 2.4 GHz | "
+               "VGPR / AGPR / SGPR | LDS bytes |", "|---|---|---|---|---|---|---|---|"]
+        entry = {"bench": line, "trace_step_us": round(step_us, 3),
+                 "trace_tflops": round(flops / (step_us * 1e-6) / 1e12, 2), "kernels": {}}
+        for k in ks:
+            c = cs.get(k["name"])
+            if c is None:
+                continue
+            ghz, busy, frac = _util_row(c)
+            if c["dispatch_ns"] < 20e3:
+                # GRBM_GUI_ACTIVE also counts the cycles around a dispatch this
+                # short, so clock and busy are not meaningful for it
+                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | — | — | — | "
+                          f"{c['vgpr']} / {c['agpr']} / {c['sgpr']} | {c['lds_bytes']} |")
+            else:
+                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | {ghz:.3f} GHz | "
+                          f"{100 * busy:.1f}% | {100 * frac:.1f}% | {c['vgpr']} / {c['agpr']} / {c['sgpr']} | "
+                          f"{c['lds_bytes']} |")
+            entry["kernels"][k["name"]] = {"trace_avg_us": round(k["avg_us"], 3), "calls": k["calls"],
+                                           "clock_ghz": round(ghz, 4), "mfma_busy": round(busy, 4),
+                                           "frac_from_counters": round(frac, 4),
+                                           **{n: c.get(n, 0) for n in UTIL_COUNTERS}}
+        md += ["", "Clock = GRBM_GUI_ACTIVE / 8 XCDs over the dispatch's own duration in the counter pass; MFMA busy = "
+                   "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over those cycles (— for a dispatch under 20 us, where "
+                   "the counter window is longer than the kernel); VGPR as rocprofv3 records it (4 registers per "
+                   "granule where gfx950 wave64 allocates 8: 128 shown = 256 allocated).", "",
+               f"Kernel-trace time per step (sum of the kernels' averages): {step_us:.2f} us = "
+                   f"{flops / (step_us * 1e-6) / 1e12:.1f} TFLOP/s.", "", "Commands:", "",
+               f"    python3 bench.py --only {wl} --variant {form} --steps {steps} --warmup 5",
+               f"    {tcmd}", f"    {ucmd}", ""]
+        fig["forms"][tag] = entry
+    path = args.summary or os.path.join(args.out, "forms.md")
+    with open(path, "w") as f:
+        f.write("\n".join(md))
+    print("\n".join(md), flush=True)
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(fig, f, indent=1)
+
+
+CLI = os.path.join(ROOT, "fmha_native_amd", "bench_fmha_fwd")
+SHORT_ROWS = 262144  # B * S * H for every short shape
+
+
+def _cli_avg(stdout, key):
+    for l in stdout.splitlines():
+        if l.startswith(key):
+            return float(l.split()[len(key.split())])
+    raise RuntimeError(f"no '{key}' line")
+
+
+def profile_short(args):
+    """Short sequences through the bench CLI: kernel trace per shape and form."""
+    shapes = [(m, 16384 // sq, sq) for m in (0, 1) for sq in (64, 128, 256, 512)]
+    md = ["# Short sequences: achieved HBM bandwidth (MI355X, one GPU)", "",
+          "Every figure from one run of `python -m fmha_native_amd.rocprof --short` on one box (repo root, "
+          "`TMPDIR=/tmp`); each pass is its own process under `timeout -s KILL`:", "",
+          "    rocprofv3 --kernel-trace --stats -d <out>/<tag> -o run -- fmha_native_amd/bench_fmha_fwd "
+          "-b <B> -h 16 -s <S> --mask <0|1> --lse 1 --dist normal --warmup 5 --iters 100 --variant <auto|regular>",
+          "", "Every shape holds the same 262,144 query rows (B·S = 16,384, H = 16), so the algorithmic HBM traffic "
+          "is the same: Q, K, V read once and O written once, 4·B·H·S·64·2 bytes, plus the 4-byte LSE per row, "
+          "135.3 MB. GB/s = those bytes ÷ the kernel's average dispatch duration (`top_kernels`, 205 dispatches: "
+          "5 warm-up, 100 timed one by one, 100 back to back); the percentage is of MI355X's 8 TB/s. `auto` is "
+          "the launcher's choice.", ""]
+    # device copies of the same traffic: 2 x 67.1 MB (read + write) and a 3:1 read/write mix
+    db, _l, ccmd = _run("short_copy", ["--kernel-trace", "--stats"],
+                        _bench("--copy-probe-mib", "64", "--steps", "100"), args.out, 120)
+    copy = [k for k in _kernel_stats(db)]
+    cp = max(copy, key=lambda k: k["calls"])
+    nbytes = 2 * (64 << 20)
+    md += [f"Device copy of 64 MiB (134.2 MB moved, `{cp['name']}`): {cp['avg_us']:.2f} us per copy = "
+           f"{nbytes / (cp['avg_us'] * 1e-6) / 1e9:,.0f} GB/s ({100 * nbytes / (cp['avg_us'] * 1e-6) / 8e12:.0f} % of "
+           f"8 TB/s): the rate a plain stream of this size reaches.", "", f"    {ccmd}", "",
+           "| shape | form | kernel | avg µs | GB/s | of 8 TB/s | of the copy rate | TFLOP/s |",
+           "|---|---|---|---|---|---|---|---|"]
+    io = 4 * SHORT_ROWS * 64 * 2 + 4 * SHORT_ROWS
+    copy_gbs = nbytes / (cp["avg_us"] * 1e-6) / 1e9
+    res = {}
+    for m, b, sq in shapes:
+        for form in ("auto", "regular"):
+            tag = f"short_m{m}_b{b}_s{sq}_{form}"
+            d = os.path.join(args.out, tag)
+            cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--kernel-trace", "--stats", "-d", d, "-o", "run",
+                   "--", CLI, "-b", str(b), "-h", "16", "-s", str(sq), "--mask", str(m), "--lse", "1", "--dist",
+                   "normal", "--warmup", "5", "--iters", "100", "--variant", form]
+            print(f"[rocprof] {tag}", flush=True)
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            dbs = glob.glob(os.path.join(d, "**", "*_results.db"), recursive=True)
+            if not dbs or "Avg:" not in r.stdout:
+                raise RuntimeError(f"{tag} failed (rc={r.returncode}): {r.stderr[-500:]}")
+            k = [k for k in _kernel_stats(dbs[0]) if k["name"].startswith("fmha_fwd")][0]
+            gbs = io / (k["avg_us"] * 1e-6) / 1e9
+            flops = 4.0 * b * 16 * sq * sq * 64 * (0.5 if m else 1.0)
+            res[(m, sq, form)] = k["avg_us"]
+            md.append(f"| {'causal' if m else 'dense'} B{b} H16 S{sq} | {form} | `{k['name']}` | {k['avg_us']:.2f} | "
+                      f"{gbs:,.0f} | {100 * gbs / 8000:.0f} % | {100 * gbs / copy_gbs:.0f} % | "
+                      f"{flops / (k['avg_us'] * 1e-6) / 1e12:.0f} |")
+    # cfg1: the kernel's duration beside the per-call times of unprofiled runs
+    md += ["", "## cfg1 (B1 H2 S128 + LSE): kernel duration and per-call time", "",
+           "| form | kernel | kernel-trace avg |", "|---|---|---|"]
+    cli_args = ["-b", "1", "-h", "2", "-s", "128", "--mask", "0", "--lse", "1", "--dist", "normal", "--warmup", "5",
+                "--iters", "100"]
+    for form in ("auto", "regular", "short"):
+        tag = f"cfg1_{form}"
+        d = os.path.join(args.out, tag)
+        cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--kernel-trace", "--stats", "-d", d, "-o", "run", "--",
+               CLI, *cli_args, "--variant", form]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        dbs = glob.glob(os.path.join(d, "**", "*_results.db"), recursive=True)
+        if not dbs or "Avg:" not in r.stdout:
+            raise RuntimeError(f"{tag} failed (rc={r.returncode}): {r.stderr[-500:]}")
+        k = [k for k in _kernel_stats(dbs[0]) if k["name"].startswith("fmha_fwd")][0]
+        md.append(f"| {form} | `{k['name']}` | {k['avg_us']:.2f} us |")
+    r = subprocess.run(["timeout", "-s", "KILL", "120", CLI, *cli_args], capture_output=True, text=True)
+    b = subprocess.run(["timeout", "-s", "KILL", "300", *_bench("--only", "cfg1", "--steps", "2000", "--warmup", "20")],
+                       capture_output=True, text=True)
+    line = json.loads([l for l in b.stdout.splitlines() if l.startswith("{")][-1])
+    md += ["", "Per-call time of the launcher's choice, unprofiled:", "",
+           "| protocol | per call |", "|---|---|",
+           f"| `bench.py --only cfg1 --steps 2000`: back to back between two events (the `bench.py` value) | "
+           f"{line['ms_per_step'] * 1e3:.2f} us |",
+           f"| same run, the reference's protocol: events around each launch, synchronised per launch | "
+           f"{line['reference_protocol_ms'] * 1e3:.2f} us |",
+           f"| the CLI, `bench_fmha_fwd {' '.join(cli_args)}`: `Avg:` (the reference's protocol, printed to "
+           f"1 us) | {_cli_avg(r.stdout, 'Avg:') * 1e3:.0f} us |",
+           f"| the CLI: `back-to-back avg:` | {_cli_avg(r.stdout, 'back-to-back avg:') * 1e3:.0f} us |", "",
+           "The launch is latency-bound: 0.13 MB moved. Back to back the launches overlap the host's submission "
+           "of the next one; the reference's protocol adds the host's launch latency to every call.", ""]
+    path = args.summary or os.path.join(args.out, "short.md")
+    with open(path, "w") as f:
+        f.write("\n".join(md))
+    print("\n".join(md), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "prof"))
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
     ap.add_argument("--json", default=None, help="also write the figures bench.py quotes here")
     ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--forms", default=None,
+                    help="profile these workload:form pairs instead (e.g. cfg4:auto,cfg5:auto,cfg5:regular)")
+    ap.add_argument("--short", action="store_true", help="profile the short-sequence shapes and cfg1 instead")
     args = ap.parse_args()
     os.makedirs(args.out, exist_ok=True)
+    if args.short:
+        profile_short(args)
+        return
+    if args.forms:
+        profile_forms(args)
+        return
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on cfg2 (dense B4 H16 S2048) and cfg3 (causal B1 H16 "
           "S8192 + LSE)", "",
           "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof` on one box "

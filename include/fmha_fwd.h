@@ -129,6 +129,11 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         into the next; its queue counters live in the
  *                         library (device memory it owns, no allocation per
  *                         call; at most 64 such launches in flight per device)
+ *   FMHA_VARIANT_SHORT    seqlen_k <= 128 only (varlen: seqlen_k must bound
+ *                         every sequence's key length): the regular grid with
+ *                         all keys loaded at once, four blocks per compute
+ *                         unit; the automatic choice for dense launches with
+ *                         seqlen_k <= 128
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
@@ -141,6 +146,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_PAIR 3
 #define FMHA_VARIANT_PERSISTENT 4
 #define FMHA_VARIANT_BALANCED 5 /* fmha_fwd_d64_bf16_ws only: it needs a workspace */
+#define FMHA_VARIANT_SHORT 6
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
@@ -284,6 +290,12 @@ __global__ void fmha_fwd_d64_bf16_pair_msk0(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params);
+/* Short forms (no counterpart in the reference): the regular grid and
+ * block for seqlen_k <= 128; 32 KiB of LDS. */
+__global__ void fmha_fwd_d64_bf16_short_msk0(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_short_msk1(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_short_msk0_varlen(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_short_msk1_varlen(FmhaFwdParams params);
 /* Tile-major causal dense forms (no counterpart in the reference): grid
  * (nhead_q, batch, tiles), tiles = ceil(seqlen_q/kM0) (pair form: pairs of
  * them), block kBlockSize (regular) or FMHA_SPLIT_KBLOCK; block z runs M-tile

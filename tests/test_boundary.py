@@ -192,8 +192,8 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    # 0-4 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
-    for bad in (-1, 5, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 5):
+    # 0-4 and 6 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
+    for bad in (-1, 5, 7, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 7):  # 5: balanced needs the workspace entry
         assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
     bad_p = _mut(q=None)
     assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID
@@ -216,8 +216,31 @@ def _shape(batch, heads, seqlen):
 R, S, P = fmha.VARIANT_REGULAR, fmha.VARIANT_SPLITKV, fmha.VARIANT_PAIR
 
 
+def test_short_form_rule():
+    """Dense launches whose keys fit two 64-key tiles take the short form
+    (their seqlen_k is exact) once they hold two blocks' worth of query rows
+    per compute unit (2 x CUs x 128 rows); smaller grids and varlen ones keep
+    the grid-shape rule (a varlen seqlen_k is only a bound the caller gives);
+    an explicit short launch with more keys is refused."""
+    # valid_params: 4 heads x 128 query rows per batch -> 512 rows
+    for sk, batch, cus, short in ((1, 128, 256, True), (64, 128, 256, True), (128, 128, 256, True),
+                                  (128, 127, 256, False), (129, 128, 256, False), (128, 152, 304, True),
+                                  (128, 151, 304, False), (128, 4096, 256, True)):
+        for causal in (0, 1):
+            got = fmha.pick_variant(_mut(seqlen_k=sk, lse=None), batch, causal, cus)
+            assert (got == fmha.VARIANT_SHORT) if short else (got in (R, S, P)), (sk, batch, cus, causal, got)
+    assert fmha.pick_variant(valid_params(varlen=True, lse=False), 4096, 1, 256) in (R, S, P)
+    lib = fmha.load_library()
+    assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(_mut(seqlen_k=129)), 1, 0, fmha.VARIANT_SHORT, None) == INVALID
+
+
 @pytest.mark.parametrize("batch,heads,seqlen,causal,cus,form", [
     (1, 8, 4096, 0, 256, S),     # 256 blocks: at most one per CU
+    (1, 2, 4096, 0, 256, S),     # 64 blocks
+    (1, 32, 1024, 0, 256, R),    # 256 blocks, but 1024 keys: halves too short
+    (1, 64, 512, 1, 256, R),
+    (1, 2, 256, 0, 256, R),      # 4 blocks, 4 key tiles
+    (1, 2, 2048, 1, 256, S),     # 2048 keys: split
     (1, 12, 4096, 0, 256, R),    # 384 dense blocks
     (1, 12, 4096, 1, 256, S),    # 384 causal blocks = 1.5 per CU: still split
     (1, 13, 4096, 1, 256, R),    # 416 causal blocks, short M-tiles
@@ -268,9 +291,11 @@ def test_rules_at_extreme_counts():
     big = 2**31 - 1
     p = valid_params(lse=False)
     p.nhead_q = p.nhead_k = big
+    p.seqlen_k = 256  # past the short form's 128 keys
     assert fmha.tile_major(p, 65535, 1) == 0
     assert fmha.pick_variant(p, 65535, 1, 256) == R
     q = valid_params(lse=False)
+    q.seqlen_q = q.seqlen_k = 4096                    # long enough for the split-KV form
     assert fmha.pick_variant(q, 1, 1, big) == S       # every grid fits such a device at once
     q.seqlen_k = 0
     assert fmha.tile_major(q, 65535, 1) == 1          # no K/V at all
@@ -291,7 +316,8 @@ def test_auto_form_rejects_what_the_launch_rejects():
     assert fmha.pick_variant(_mut(q=None), 1, 0, 256) == -1
     assert fmha.pick_variant(valid_params(), 1, 2, 256) == -1
     assert fmha.pick_variant(valid_params(), 1, 0, -1) == -1
-    assert fmha.pick_variant(valid_params(), 1, 0) in (R, S, P)  # the current device's count
+    assert fmha.pick_variant(valid_params(), 4096, 0) == fmha.VARIANT_SHORT  # 128 keys, 2M query rows
+    assert fmha.pick_variant(_mut(seqlen_k=129), 1, 0) in (R, S, P)  # the current device's count
 
 
 # ---------------------------------------------------------------- bench contract

@@ -6,7 +6,8 @@ s_barrier of every entry, the wave has no LDS read in flight (an
 ``s_waitcnt lgkmcnt(0)`` follows the last ds_read).  A read left in flight
 would race with the other waves' DMA refill of its stage right after the
 barrier.  Also: no entry spills to scratch, and every entry keeps two waves
-per SIMD.
+per SIMD (the short form four).  The short form's first wait counts on the
+order its loads are issued in (K, Q, V), which is checked too.
 """
 import os
 import re
@@ -51,6 +52,9 @@ def test_every_entry_compiled(asm):
         assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
     for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_merge"):
         assert any(e in n for n in names), e
+    for m in (0, 1):
+        for v in ("", "_varlen"):
+            assert any(f"fmha_fwd_d64_bf16_short_msk{m}{v}13FmhaFwdParams" in n for n in names), (m, v)
 
 
 def test_no_lds_read_in_flight_at_barriers(asm):
@@ -75,3 +79,33 @@ def test_no_scratch_and_two_waves_per_simd(asm):
     occupancy = re.findall(r"; Occupancy: (\d+)", asm)
     assert scratch and all(int(s) == 0 for s in scratch), scratch
     assert occupancy and all(int(o) >= 2 for o in occupancy), occupancy
+
+
+def _occupancy(src):
+    """Occupancy (waves per SIMD) of every function from its kernel-info block."""
+    occ = {}
+    for m in re.finditer(r"^\s*\.set\s+(_Z[^.\s]+)\.has_indirect_call.*?; Occupancy: (\d+)", src, re.M | re.S):
+        occ[m.group(1)] = int(m.group(2))
+    return occ
+
+
+def test_short_form_issue_order_and_occupancy(asm):
+    """The short form issues its K loads into LDS, then Q into registers,
+    then V into LDS, and waits vmcnt(4) before its first barrier: that wait
+    covers K and Q only when the four V loads are the last ones issued.  It
+    keeps four waves per SIMD (four blocks per compute unit)."""
+    occ = _occupancy(asm)
+    shorts = {n: b for n, b in _functions(asm).items() if "_short_msk" in n}
+    assert len(shorts) == 4
+    for name, body in shorts.items():
+        assert occ.get(name) == 4, (name, occ.get(name))
+        seq = []
+        for line in body.splitlines():
+            ins = line.strip()
+            if ins.startswith("buffer_load_dwordx4"):
+                seq.append("L" if ins.endswith(" lds") else "R")
+            elif ins.startswith("s_barrier"):
+                break
+            elif ins.startswith("s_waitcnt") and "vmcnt" in ins:
+                seq.append(re.search(r"vmcnt\((\d+)\)", ins).group(0))
+        assert seq == ["L"] * 4 + ["R"] * 4 + ["L"] * 4 + ["vmcnt(4)"], (name, seq)

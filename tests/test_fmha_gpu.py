@@ -42,7 +42,7 @@ FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair
          "persistent": fmha.VARIANT_PERSISTENT}
 # the balanced form (causal dense, through the workspace entry) runs on the
 # matrices of reference cases and benchmark configurations
-MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED)
+MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, short=fmha.VARIANT_SHORT)
 
 
 def _dense_only(form, prob):
@@ -50,6 +50,8 @@ def _dense_only(form, prob):
         pytest.skip("the persistent form takes dense problems only")
     if form == "balanced" and (prob.varlen or not prob.causal):
         pytest.skip("the balanced form takes causal dense problems only")
+    if form == "short" and prob.seqlen_k > 128:
+        pytest.skip("the short form takes at most 128 keys")
 
 
 @pytest.mark.parametrize("form", list(MATRIX_FORMS))
