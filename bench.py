@@ -383,8 +383,11 @@ def main():
 
         prob, mult = {"cfg2": (cfg2, 1.0), "cfg3": (cfg3, 1.0)}.get(args.only) or baseline_problems()[args.only]
         r = time_problem(prob, args.steps, args.warmup, torch, mult, fmha.VARIANTS[args.variant])
+        # launch order, for a profiler's trace: ramp, warmup, steps timed back
+        # to back, then as many under the reference's protocol
         print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"], "form": r["form"],
-                          "reference_protocol_ms": r["ref_ms"]}), flush=True)
+                          "reference_protocol_ms": r["ref_ms"], "ramp_launches": r["ramp"], "warmup": args.warmup,
+                          "steps": args.steps}), flush=True)
         return
     r2 = time_problem(cfg2, args.steps, args.warmup, torch)
     r3 = time_problem(cfg3, max(1, args.steps // 2), max(1, args.warmup // 2), torch)

@@ -94,6 +94,24 @@ def _kernel_stats(db):
     return [dict(name=n, calls=c, avg_us=a) for n, c, _t, a, _p in con.execute("select * from top_kernels")]
 
 
+def _timed_stats(db, line):
+    """Per-kernel average duration (us) of the dispatches bench.py --only
+    timed back to back (after its ramp and warm-up launches; each step is one
+    dispatch of every kernel of the form), from the trace's own timestamps."""
+    con = sqlite3.connect(db)
+    per = defaultdict(list)
+    for name, t0, t1 in con.execute("select name, start, end from kernels order by start"):
+        if name.startswith("fmha_fwd"):
+            per[name].append((t1 - t0) / 1e3)
+    first = line["ramp_launches"] + line["warmup"]
+    out = {}
+    for name, d in per.items():
+        timed = d[first:first + line["steps"]]
+        if len(timed) == line["steps"]:
+            out[name] = sum(timed) / len(timed)
+    return out
+
+
 def _counters(db, kernel_prefix="fmha_fwd"):
     """Per-dispatch counter values (summed over the chip), averaged over the
     dispatches of each kernel after its first; also the dispatches' own
@@ -161,6 +179,9 @@ def profile_forms(args):
                                _bench("--only", wl, "--variant", form, "--steps", steps, "--warmup", "5"),
                                args.out, 300)
         ks = [k for k in _kernel_stats(db) if k["name"].startswith("fmha_fwd")]
+        timed = _timed_stats(db, tline)
+        for k in ks:
+            k["avg_all_us"], k["avg_us"] = k["avg_us"], timed.get(k["name"], k["avg_us"])
         step_us = sum(k["avg_us"] for k in ks)
         # counters
         udb, _l, ucmd = _run(f"pmc_util_{tag}", ["--pmc", *UTIL_COUNTERS],
@@ -172,7 +193,7 @@ def profile_forms(args):
                f"{line['tflops']:.1f} TFLOP/s ({100 * line['tflops'] / PEAK_BF16_TFLOPS:.1f}% of 2516.6)"
                + (f"; exact-count {prob.exact_flops() / (line['ms_per_step'] * 1e-3) / 1e12:.1f} TFLOP/s"
                   if prob.varlen else "") + ".", "",
-               "| kernel | dispatches | trace avg | clock | MFMA busy | MFMA busy × clock / 2.4 GHz | "
+               "| kernel | dispatches | trace avg, timed (all) | clock | MFMA busy | MFMA busy × clock / 2.4 GHz | "
                "VGPR / AGPR / SGPR | LDS bytes |", "|---|---|---|---|---|---|---|---|"]
         entry = {"bench": line, "trace_step_us": round(step_us, 3),
                  "trace_tflops": round(flops / (step_us * 1e-6) / 1e12, 2), "kernels": {}}
@@ -184,10 +205,10 @@ def profile_forms(args):
             if c["dispatch_ns"] < 20e3:
                 # GRBM_GUI_ACTIVE also counts the cycles around a dispatch this
                 # short, so clock and busy are not meaningful for it
-                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | — | — | — | "
+                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | — | — | — | "
                           f"{c['vgpr']} / {c['agpr']} / {c['sgpr']} | {c['lds_bytes']} |")
             else:
-                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | {ghz:.3f} GHz | "
+                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | {ghz:.3f} GHz | "
                           f"{100 * busy:.1f}% | {100 * frac:.1f}% | {c['vgpr']} / {c['agpr']} / {c['sgpr']} | "
                           f"{c['lds_bytes']} |")
             entry["kernels"][k["name"]] = {"trace_avg_us": round(k["avg_us"], 3), "calls": k["calls"],
@@ -350,8 +371,11 @@ def main():
 
     # 1. kernel trace
     md += ["## Kernel trace (average dispatch duration vs bench.py's HIP events in the same process)", "",
-           "| workload | kernel | dispatches | rocprofv3 avg | bench.py HIP-event avg | TFLOP/s (trace) | % of 2516.6 |",
-           "|---|---|---|---|---|---|---|"]
+           "`timed` = the dispatches bench.py timed back to back (after its 0.1 s clock ramp and warm-up); `all` = "
+           "every dispatch of the run, the ramp's included.", "",
+           "| workload | kernel | dispatches | rocprofv3 avg, timed | rocprofv3 avg, all | bench.py HIP-event avg | "
+           "TFLOP/s (trace, timed) | % of 2516.6 |",
+           "|---|---|---|---|---|---|---|---|"]
     cmds = []
     trace = {}
     for wl in ("cfg2", "cfg3"):
@@ -360,10 +384,12 @@ def main():
                               _bench("--only", wl, "--steps", str(steps), "--warmup", "10"), args.out, 300)
         cmds.append(cmd)
         k = [s for s in _kernel_stats(db) if s["name"].startswith("fmha_fwd")][0]
-        tf = WORKLOADS[wl]["flops"] / (k["avg_us"] * 1e-6) / 1e12
-        trace[wl] = {"kernel": k["name"], "avg_us": k["avg_us"], "bench_us": pline["ms_per_step"] * 1e3, "tflops": tf}
-        md.append(f"| {wl} | `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} us | {pline['ms_per_step'] * 1e3:.2f} us "
-                  f"| {tf:.1f} | {100 * tf / PEAK_BF16_TFLOPS:.1f}% |")
+        timed = _timed_stats(db, pline)[k["name"]]
+        tf = WORKLOADS[wl]["flops"] / (timed * 1e-6) / 1e12
+        trace[wl] = {"kernel": k["name"], "avg_us": timed, "avg_all_us": k["avg_us"],
+                     "bench_us": pline["ms_per_step"] * 1e3, "tflops": tf}
+        md.append(f"| {wl} | `{k['name']}` | {k['calls']} | {timed:.2f} us | {k['avg_us']:.2f} us | "
+                  f"{pline['ms_per_step'] * 1e3:.2f} us | {tf:.1f} | {100 * tf / PEAK_BF16_TFLOPS:.1f}% |")
     md += ["", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
 
     # 2. traffic
@@ -445,6 +471,7 @@ def main():
             "bench_ms_per_step": bench[wl]["ms_per_step"],
             "bench_tflops": bench[wl]["tflops"],
             "trace_avg_us": round(trace[wl]["avg_us"], 3),
+            "trace_avg_all_dispatches_us": round(trace[wl]["avg_all_us"], 3),
             "trace_tflops": round(trace[wl]["tflops"], 2),
             "trace_bench_us": round(trace[wl]["bench_us"], 3),
             "counter_dispatch_us": round(c["dispatch_ns"] / 1e3, 3),
