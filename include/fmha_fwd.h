@@ -112,12 +112,15 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 
 /* The same launch with the kernel form chosen by the caller (this build's
  * own; no counterpart in the reference):
- *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: split-KV when the
- *                         regular grid has at most one block per compute unit
- *                         (causal: at most 1.5, or up to 2 with seqlen_k >= 8192);
- *                         pair when its blocks fill whole rounds of the compute
- *                         units and seqlen_k >= 8192 (causal: >= 32768); else
- *                         the regular entries
+ *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: short for dense
+ *                         launches with seqlen_k <= 128 and at least
+ *                         2 x CUs x 128 query rows; with seqlen_k >= 2048,
+ *                         split-KV when the regular grid has at most one
+ *                         block per compute unit (causal: at most 1.5, or up
+ *                         to 2 with seqlen_k >= 8192); pair when its blocks
+ *                         fill whole rounds of the compute units and
+ *                         seqlen_k >= 8192 (causal: >= 32768); else the
+ *                         regular entries
  *   FMHA_VARIANT_REGULAR  the four reference-named entries (kBlockSize threads)
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
@@ -130,10 +133,10 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         library (device memory it owns, no allocation per
  *                         call; at most 64 such launches in flight per device)
  *   FMHA_VARIANT_SHORT    seqlen_k <= 128 only (varlen: seqlen_k must bound
- *                         every sequence's key length): the regular grid with
- *                         all keys loaded at once, four blocks per compute
- *                         unit; the automatic choice for dense launches with
- *                         seqlen_k <= 128
+ *                         every sequence's key length; keys past the first
+ *                         128 of a longer sequence are not read): the
+ *                         regular grid with all keys loaded at once, four
+ *                         blocks per compute unit
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
