@@ -11,8 +11,8 @@
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
 //   --variant auto|regular|splitkv|pair|persistent|balanced|short   kernel form (default: the launcher's choice)
-//   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws), so the automatic choice may be
-//                    the balanced causal form; --variant balanced implies it
+//   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws, allocated before timing), so the
+//                    automatic choice may be the balanced causal form (default 1); --variant balanced needs it
 //   --order auto|reference   causal block order (reference: batch after batch)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
@@ -47,7 +47,7 @@ struct Config {
     std::string dist = "ref";
     int variant = FMHA_VARIANT_AUTO;
     bool reference_order = false;
-    bool workspace = false;
+    bool workspace = true;
     float scale_inputs = 1.0f;
     std::vector<int> varlen_seqs;
 };
@@ -69,7 +69,7 @@ static void usage(const char* prog) {
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
            "  --variant V      auto|regular|splitkv|pair|persistent|balanced|short form [auto]\n"
-           "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [0]\n"
+           "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [1]\n"
            "  --order O        auto|reference causal block order [auto]\n",
            prog);
 }
