@@ -17,11 +17,14 @@ exact command of every pass:
 2. HBM traffic of cfg2 and cfg3: FETCH_SIZE and WRITE_SIZE per dispatch, each
    scaled by what the counter reads for a device copy of known size
    (bench.py ``--copy-probe-mib``), against the algorithmic bytes;
-3. utilisation of cfg2 and cfg3: clock (GRBM_GUI_ACTIVE cycles over the same
-   dispatch's own duration), MFMA busy cycles, VALU/MFMA/LDS instruction
-   counts, LDS bank conflicts, plus the VGPR/AGPR/SGPR/LDS allocation the
-   profiler records for the dispatch.  MFMA busy x clock / 2.4 GHz is the
-   fraction of the 2516.6 TFLOP/s peak those dispatches reach, a check on the
+3. utilisation of cfg2 and cfg3: the cycles the shader engines had waves
+   (SQ_BUSY_CYCLES over the engine count: the kernel's span in shader
+   clocks), the MFMA busy fraction of those cycles, a lower bound on the clock
+   (those cycles over the dispatch's duration, which also holds the launch's
+   set-up and drain), VALU/MFMA/LDS instruction counts, LDS bank conflicts,
+   plus the VGPR/AGPR/SGPR/LDS allocation the profiler records for the
+   dispatch.  MFMA cycles per SIMD over (duration x 2.4 GHz) is the fraction
+   of the 2516.6 TFLOP/s peak those dispatches reach, a check on the
    HIP-event figure that needs no timer.
 
 The JSON (``--json``) carries the figures ``bench.py`` quotes in its
@@ -57,6 +60,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PEAK_BF16_TFLOPS = 2516.6
 NUM_XCD = 8
 NUM_SIMD = 256 * 4
+NUM_SE = 32  # shader engines (8 XCDs x 4); read from the profiler's agent record where present
 
 UTIL_COUNTERS = ["GRBM_GUI_ACTIVE", "SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU",
                  "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_VALU_TRANS_F32"]
@@ -143,12 +147,35 @@ def _counters(db, kernel_prefix="fmha_fwd"):
     return out
 
 
-def _util_row(c):
-    """clock (GHz), MFMA busy fraction, fraction of the bf16 peak."""
-    cycles_xcd = c["GRBM_GUI_ACTIVE"] / NUM_XCD
-    ghz = cycles_xcd / c["dispatch_ns"]
-    busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMD / cycles_xcd
-    return ghz, busy, busy * ghz / 2.4
+def _num_se(db):
+    """Shader engines of the profiled GPU (the agent record's
+    num_shader_banks), else NUM_SE."""
+    try:
+        con = sqlite3.connect(db)
+        for (ext,) in con.execute("select extdata from rocpd_info_agent where type = 'GPU'"):
+            n = json.loads(ext or "{}").get("num_shader_banks")
+            if n:
+                return int(n)
+    except sqlite3.Error:
+        pass
+    return NUM_SE
+
+
+def _util_row(c, n_se=NUM_SE):
+    """(clock lower bound in GHz, MFMA busy fraction of the cycles the
+    shader engines had waves, fraction of the bf16 peak).
+
+    SQ_BUSY_CYCLES summed over the engines, divided by their count, is the
+    kernel's span in shader clocks; the dispatch duration the profiler
+    records also holds the launch's set-up and drain, so cycles over duration
+    bound the clock from below.  (GRBM_GUI_ACTIVE / 8 over the duration
+    counts outside the waves' span and reads above the clock the kernel
+    measures itself with s_memtime against s_memrealtime.)  The fraction of
+    peak needs no clock: MFMA cycles per SIMD over duration x 2.4 GHz."""
+    active = c["SQ_BUSY_CYCLES"] / n_se
+    ghz = active / c["dispatch_ns"]
+    mfma_per_simd = c["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMD
+    return ghz, mfma_per_simd / active, mfma_per_simd / (c["dispatch_ns"] * 2.4)
 
 
 def profile_forms(args):
@@ -187,13 +214,14 @@ def profile_forms(args):
         udb, _l, ucmd = _run(f"pmc_util_{tag}", ["--pmc", *UTIL_COUNTERS],
                              _bench("--only", wl, "--variant", form, "--steps", "5", "--warmup", "1"), args.out, 120)
         cs = _counters(udb)
+        n_se = _num_se(udb)
         flops = prob.flops()
         md += [f"## {wl} ({prob.name}), form `{form}` → {line['form']}", "",
                f"bench.py (back-to-back HIP events): {line['ms_per_step'] * 1e3:.2f} us per step, "
                f"{line['tflops']:.1f} TFLOP/s ({100 * line['tflops'] / PEAK_BF16_TFLOPS:.1f}% of 2516.6)"
                + (f"; exact-count {prob.exact_flops() / (line['ms_per_step'] * 1e-3) / 1e12:.1f} TFLOP/s"
                   if prob.varlen else "") + ".", "",
-               "| kernel | dispatches | trace avg, timed (all) | clock | MFMA busy | MFMA busy × clock / 2.4 GHz | "
+               "| kernel | dispatches | trace avg, timed (all) | clock ≥ | MFMA busy | fraction of peak | "
                "VGPR / AGPR / SGPR | LDS bytes |", "|---|---|---|---|---|---|---|---|"]
         entry = {"bench": line, "trace_step_us": round(step_us, 3),
                  "trace_tflops": round(flops / (step_us * 1e-6) / 1e12, 2), "kernels": {}}
@@ -201,10 +229,10 @@ def profile_forms(args):
             c = cs.get(k["name"])
             if c is None:
                 continue
-            ghz, busy, frac = _util_row(c)
+            ghz, busy, frac = _util_row(c, n_se)
             if c["dispatch_ns"] < 20e3:
-                # GRBM_GUI_ACTIVE also counts the cycles around a dispatch this
-                # short, so clock and busy are not meaningful for it
+                # a dispatch this short is mostly set-up and drain: clock and
+                # busy are not meaningful for it
                 md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | — | — | — | "
                           f"{c['vgpr']} / {c['agpr']} / {c['sgpr']} | {c['lds_bytes']} |")
             else:
@@ -215,10 +243,11 @@ def profile_forms(args):
                                            "clock_ghz": round(ghz, 4), "mfma_busy": round(busy, 4),
                                            "frac_from_counters": round(frac, 4),
                                            **{n: c.get(n, 0) for n in UTIL_COUNTERS}}
-        md += ["", "Clock = GRBM_GUI_ACTIVE / 8 XCDs over the dispatch's own duration in the counter pass; MFMA busy = "
-                   "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over those cycles (— for a dispatch under 20 us, where "
-                   "the counter window is longer than the kernel); VGPR as rocprofv3 records it (4 registers per "
-                   "granule where gfx950 wave64 allocates 8: 128 shown = 256 allocated).", "",
+        md += ["", "Per dispatch of the counter pass: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the cycles "
+                   "the shader engines had waves (SQ_BUSY_CYCLES / engines); clock ≥ those cycles over the dispatch's "
+                   "duration; fraction of peak = MFMA cycles per SIMD over duration × 2.4 GHz (— for a dispatch under "
+                   "20 us); VGPR as rocprofv3 records it (4 registers per granule where gfx950 wave64 allocates 8: "
+                   "128 shown = 256 allocated).", "",
                f"Kernel-trace time per step (sum of the kernels' averages): {step_us:.2f} us = "
                    f"{flops / (step_us * 1e-6) / 1e12:.1f} TFLOP/s.", "", "Commands:", "",
                f"    python3 bench.py --only {wl} --variant {form} --steps {steps} --warmup 5",
@@ -429,9 +458,13 @@ def main():
 
     # 3. utilisation, with the clock from each dispatch's own duration
     md += ["## Utilisation counters (per dispatch, summed over the chip)", "",
-           "Clock = GRBM_GUI_ACTIVE / 8 XCDs over the same dispatches' duration in this pass; MFMA busy = "
-           "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over those cycles; MFMA busy x clock / 2.4 GHz = fraction of "
-           "the 2516.6 TFLOP/s peak (2.4 GHz is the clock that figure assumes).", ""]
+           "Active cycles = SQ_BUSY_CYCLES / shader engines: the kernel's span in shader clocks (waves present). MFMA "
+           "busy = SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs over the active cycles. Clock ≥ active cycles over the "
+           "dispatch's duration in this pass (the duration also holds the launch's set-up and drain). Fraction of "
+           "peak = MFMA cycles per SIMD over duration × 2.4 GHz (the clock the 2516.6 TFLOP/s figure assumes), "
+           "which needs no clock estimate. GRBM_GUI_ACTIVE / 8 over the duration is not used: it counts outside the "
+           "waves' span and reads above the clock the kernel measures itself.",
+           ""]
     cmds = []
     rows = []
     for wl in ("cfg2", "cfg3"):
@@ -439,11 +472,10 @@ def main():
                               _bench("--only", wl, "--steps", "10", "--warmup", "1"), args.out, 120)
         cmds.append(cmd)
         k, c = list(_counters(db).items())[0]
-        cycles_xcd = c["GRBM_GUI_ACTIVE"] / NUM_XCD
-        ghz = cycles_xcd / c["dispatch_ns"]  # cycles per ns
-        mfma_busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMD / cycles_xcd
+        n_se = _num_se(db)
+        ghz, mfma_busy, frac = _util_row(c, n_se)
         iters = c["SQ_INSTS_MFMA"] / 16.0  # 16 MFMA per wave per 64-key tile
-        rows.append((wl, k, c, ghz, mfma_busy, iters))
+        rows.append((wl, k, c, ghz, mfma_busy, iters, frac, c["SQ_BUSY_CYCLES"] / n_se))
     md += ["| | " + " | ".join(r[0] for r in rows) + " |", "|---|" + "---|" * len(rows)]
     md.append("| kernel | " + " | ".join(f"`{r[1]}`" for r in rows) + " |")
     md.append("| VGPR / AGPR / SGPR (rocprofv3 dispatch fields) | "
@@ -451,10 +483,12 @@ def main():
     md.append("| LDS bytes per block | " + " | ".join(f"{r[2]['lds_bytes']}" for r in rows) + " |")
     md.append("| dispatch duration in this pass | " + " | ".join(f"{r[2]['dispatch_ns'] / 1e3:.2f} us" for r in rows)
               + " |")
-    md.append("| clock (GRBM_GUI_ACTIVE / 8 / duration) | " + " | ".join(f"{r[3]:.3f} GHz" for r in rows) + " |")
-    md.append("| MFMA busy (per SIMD, of kernel cycles) | " + " | ".join(f"{100 * r[4]:.1f}%" for r in rows) + " |")
-    md.append("| MFMA busy x clock / 2.4 GHz (fraction of peak) | "
-              + " | ".join(f"{100 * r[4] * r[3] / 2.4:.1f}%" for r in rows) + " |")
+    md.append("| active cycles (SQ_BUSY_CYCLES / shader engines) | "
+              + " | ".join(f"{r[7]:,.0f}" for r in rows) + " |")
+    md.append("| clock ≥ (active cycles / duration) | " + " | ".join(f"{r[3]:.3f} GHz" for r in rows) + " |")
+    md.append("| MFMA busy (per SIMD, of active cycles) | " + " | ".join(f"{100 * r[4]:.1f}%" for r in rows) + " |")
+    md.append("| fraction of peak (MFMA cycles per SIMD / (duration x 2.4 GHz)) | "
+              + " | ".join(f"{100 * r[6]:.1f}%" for r in rows) + " |")
     for name in UTIL_COUNTERS[1:]:
         md.append(f"| {name} | " + " | ".join(f"{r[2].get(name, 0):,.0f}" for r in rows) + " |")
     md.append("| VALU instr per wave per 64-key tile (incl. 16 MFMA) | "
@@ -464,7 +498,7 @@ def main():
            "wave64 allocates 8 (so 128 shown = 256 allocated: two waves per SIMD); `tests/test_codegen.py` checks "
            "the compiler's own counts.", "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
 
-    for wl, k, c, ghz, busy, _it in rows:
+    for wl, k, c, ghz, busy, _it, frac, _active in rows:
         fig[wl] = {
             "kernel": k,
             "workload": WORKLOADS[wl]["desc"],
@@ -477,7 +511,7 @@ def main():
             "counter_dispatch_us": round(c["dispatch_ns"] / 1e3, 3),
             "clock_ghz": round(ghz, 4),
             "mfma_busy": round(busy, 4),
-            "frac_from_counters": round(busy * ghz / 2.4, 4),
+            "frac_from_counters": round(frac, 4),
             "hbm_bytes_per_launch": traffic[wl]["hbm_bytes"],
             "algorithmic_bytes": traffic[wl]["algorithmic_bytes"],
             "fetch_kib_per_dispatch": traffic[wl]["fetch_kib"],

@@ -51,13 +51,30 @@ def test_timed_stats_drops_a_kernel_with_too_few_dispatches(tmp_path):
 
 
 def test_util_row():
-    # 8 XCDs x 2e5 cycles over 100 us -> 2.0 GHz; 1024 SIMDs each busy 1e5 of
-    # 2e5 cycles -> 50 %; 50 % x 2.0 / 2.4 of the peak
-    c = {"GRBM_GUI_ACTIVE": 8 * 2.0e5, "dispatch_ns": 1.0e5, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 1.0e5}
-    ghz, busy, frac = rocprof._util_row(c)
+    # 32 engines x 2e5 busy cycles -> a 2e5-cycle span; over a 100 us dispatch
+    # the clock is at least 2.0 GHz; 1024 SIMDs each busy 1e5 MFMA cycles ->
+    # 50 % of the span; of the peak: 1e5 / (1e5 ns x 2.4 GHz)
+    c = {"SQ_BUSY_CYCLES": 32 * 2.0e5, "dispatch_ns": 1.0e5, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 1.0e5,
+         "GRBM_GUI_ACTIVE": 8 * 2.5e5}
+    ghz, busy, frac = rocprof._util_row(c, 32)
     assert ghz == pytest.approx(2.0)
     assert busy == pytest.approx(0.5)
-    assert frac == pytest.approx(0.5 * 2.0 / 2.4)
+    assert frac == pytest.approx(1.0e5 / (1.0e5 * 2.4))
+    assert frac == pytest.approx(busy * ghz / 2.4)  # the identity the roofline line quotes
+
+
+def test_num_se_from_agent_record(tmp_path):
+    import json
+
+    path = tmp_path / "a.db"
+    con = sqlite3.connect(path)
+    con.execute("create table rocpd_info_agent (type text, extdata text)")
+    con.execute("insert into rocpd_info_agent values ('CPU', '{}')")
+    con.execute("insert into rocpd_info_agent values ('GPU', ?)", (json.dumps({"num_shader_banks": 16}),))
+    con.commit()
+    con.close()
+    assert rocprof._num_se(str(path)) == 16
+    assert rocprof._num_se(_db(tmp_path, [])) == rocprof.NUM_SE  # no agent table
 
 
 def test_cli_avg_parser():
