@@ -1316,6 +1316,10 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
         kv_end = e < 0 ? 0 : (e > sk ? sk : e);
     }
     const int ntiles = (kv_end + kTileN - 1) / kTileN;  // <= 2 (the launcher's rule)
+    // A varlen sequence with more keys than the form holds breaks the caller's
+    // promise (seqlen_k bounds every sequence): its rows get NaN in O and LSE
+    // instead of a softmax over its first 128 keys.
+    const bool too_long = kVarlen && ntiles > kShortTiles;
     const int wrow0 = row0 + wave * kRowsPerWave;
     const int my_row = wrow0 + l32;
 
@@ -1438,7 +1442,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
     // epilogue: O = O^T / l through this wave's rows of the K tile area (every
     // wave's K reads are done after the barrier), LSE
     const float l_tot = wave_sum_halves(l_part);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const float inv = too_long ? __builtin_nanf("") : l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     ring_barrier();
     lds_char* const tb = kl + wave * (kRowsPerWave * kRowBytes);
 #pragma unroll
@@ -1472,7 +1476,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
             lse_base = p.lse + (int64_t)h * (p.nhead_stride_q / p.stride_q) + off_q;
         else
             lse_base = p.lse + (int64_t)b * p.nhead_q * p.seqlen_q + (int64_t)h * p.seqlen_q;
-        lse_base[my_row] = (__builtin_log2f(l_tot) + m_ref) * 0.69314718055994530942f;
+        lse_base[my_row] = too_long ? __builtin_nanf("") : (__builtin_log2f(l_tot) + m_ref) * 0.69314718055994530942f;
     }
 }
 

@@ -133,10 +133,10 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         library (device memory it owns, no allocation per
  *                         call; at most 64 such launches in flight per device)
  *   FMHA_VARIANT_SHORT    seqlen_k <= 128 only (varlen: seqlen_k must bound
- *                         every sequence's key length; keys past the first
- *                         128 of a longer sequence are not read): the
- *                         regular grid with all keys loaded at once, four
- *                         blocks per compute unit
+ *                         every sequence's key length; the rows of a longer
+ *                         sequence get NaN in O and LSE): the regular grid
+ *                         with all keys loaded at once, four blocks per
+ *                         compute unit
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry

@@ -465,6 +465,42 @@ def test_persistent_rejects_varlen():
 
 
 @pytest.mark.parametrize("causal", [False, True])
+def test_short_varlen_flags_a_sequence_longer_than_the_bound(causal):
+    """A varlen launch in the short form promises (seqlen_k <= 128) that every
+    sequence has at most 128 keys; one that has more gets NaN in its O and
+    LSE rows, loudly, while the other sequences stay exact."""
+    import torch
+
+    from harness import build_params
+
+    seqs = (100, 200, 64)
+    p = Problem(batch=0, nhead_q=2, nhead_k=1, seqlen_q=0, causal=causal, lse=True, varlen_seqs=seqs)
+    q, k, v = make_inputs(p, "ref", 5)
+    nq, nk, nlse = p.sizes()
+    dev = lambda a: torch.from_numpy(a.view(np.int16)).to("cuda:0")
+    do = torch.zeros(nq, dtype=torch.int16, device="cuda:0")
+    dl = torch.zeros(nlse, dtype=torch.float32, device="cuda:0")
+    seq = torch.from_numpy(p.seqstart()).to("cuda:0")
+    prm = build_params(p, dev(q), dev(k), dev(v), do, dl, seq)
+    prm.seqlen_k = 128  # the (broken) promise: no sequence has more keys
+    print("launch: short varlen", seqs, "causal", causal, flush=True)
+    fmha.fmha_fwd_d64_bf16(prm, p.batch, int(causal), None, fmha.VARIANT_SHORT)
+    torch.cuda.synchronize()
+    o = verify.bf16_bits_to_f32(do.cpu().numpy().view(np.uint16)).reshape(2, -1, 64)
+    lse = dl.cpu().numpy().reshape(2, -1)
+    o_ref, lse_ref = oracle.run(p, q, k, v)
+    o_ref, lse_ref = o_ref.reshape(2, -1, 64), lse_ref.reshape(2, -1)
+    # rows of the 200-key sequence whose M-tile sees more than 128 keys: all of
+    # them, or (causal) those of its second M-tile; the others are exact
+    flagged = np.zeros(o.shape[1], bool)
+    flagged[100 + (128 if causal else 0):300] = True
+    assert np.all(np.isnan(o[:, flagged])) and np.all(np.isnan(lse[:, flagged]))
+    ok = ~flagged
+    assert np.all(np.abs(o[:, ok] - o_ref[:, ok]) <= 1e-2 + 1e-2 * np.abs(o_ref[:, ok]))
+    assert np.abs(lse[:, ok] - lse_ref[:, ok]).max() <= 1e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_persistent_queue_state_across_launches(causal):
     """The persistent form's queue counters are left at zero by every launch:
     launches of different shapes in a row (many items, fewer items than
