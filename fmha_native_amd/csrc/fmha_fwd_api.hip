@@ -11,7 +11,6 @@
 
 #include <algorithm>
 #include <atomic>
-#include <vector>
 
 #include "fmha_fwd.h"
 #include "fmha_internal.h"
@@ -193,21 +192,24 @@ bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, b
     if (n_items > FMHA_BALANCED_MAX_ITEMS) return false;
     if (ws_bytes) *ws_bytes = (int64_t)n_split * p->nhead_q * batch * 2 * FMHA_BALANCED_PART_BYTES;
     if (a) {
+        // a fixed table and an in-place sort: the plan allocates nothing (the
+        // allocation-free entry point runs it too); the order is total, so
+        // std::sort needs no stability
         struct It {
             int w, mt, half;
         };
-        std::vector<It> items;
-        items.reserve(n_items);
+        It items[FMHA_BALANCED_MAX_ITEMS];
+        int n = 0;
         for (int mt = 0; mt < m_tiles; ++mt) {
-            const int n = causal_ntiles(p, mt);
+            const int kt = causal_ntiles(p, mt);
             if (mt < split_from) {
-                items.push_back({n, mt, 0});
+                items[n++] = {kt, mt, 0};
             } else {
-                items.push_back({(n + 1) / 2, mt, 0});
-                items.push_back({n / 2, mt, 1});
+                items[n++] = {(kt + 1) / 2, mt, 0};
+                items[n++] = {kt / 2, mt, 1};
             }
         }
-        std::stable_sort(items.begin(), items.end(), [](const It& x, const It& y) {
+        std::sort(items, items + n, [](const It& x, const It& y) {
             if (x.w != y.w) return x.w > y.w;
             if (x.mt != y.mt) return x.mt > y.mt;
             return x.half < y.half;
