@@ -173,8 +173,46 @@ int causal_ntiles(const FmhaFwdParams* p, int mt) {
 // per resident block (otherwise the regular heaviest-first order balances
 // already).  Returns false when there is no plan (not causal dense, too many
 // items for the table); fills `a` (table, split range) when given.
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force,
+                         FmhaBalancedArgs* a, int64_t* ws_bytes);
+
+// The plan depends on the launch's shape only, so the last one built on a
+// thread is kept: a serving loop relaunching one shape skips the sort (about
+// 10 us of host time for cfg5's 531 items).
 bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force, FmhaBalancedArgs* a,
                    int64_t* ws_bytes) {
+    struct Key {
+        int seqlen_q, seqlen_k, nhead_q, batch, causal, varlen, force;
+        int64_t cus;
+        bool operator==(const Key& o) const {
+            return seqlen_q == o.seqlen_q && seqlen_k == o.seqlen_k && nhead_q == o.nhead_q && batch == o.batch &&
+                   causal == o.causal && varlen == o.varlen && force == o.force && cus == o.cus;
+        }
+    };
+    thread_local Key last_key{-1, -1, -1, -1, -1, -1, -1, -1};
+    thread_local bool last_ok = false;
+    thread_local int64_t last_bytes = 0;
+    thread_local FmhaBalancedArgs last_plan;
+    const Key key{p->seqlen_q, p->seqlen_k, p->nhead_q, batch, causal, p->seqstart_q != nullptr ? 1 : 0,
+                  force ? 1 : 0, cus};
+    if (!(key == last_key)) {
+        last_ok = balanced_plan_build(p, batch, causal, cus, force, &last_plan, &last_bytes);
+        last_key = key;
+    }
+    if (!last_ok) return false;
+    if (ws_bytes) *ws_bytes = last_bytes;
+    if (a) {
+        a->split_from = last_plan.split_from;
+        a->n_split = last_plan.n_split;
+        a->n_items = last_plan.n_items;
+        a->pad = 0;
+        std::copy(last_plan.item, last_plan.item + last_plan.n_items, a->item);
+    }
+    return true;
+}
+
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force,
+                         FmhaBalancedArgs* a, int64_t* ws_bytes) {
     if (!causal || p->seqstart_q != nullptr || batch <= 0 || p->seqlen_q <= 0 || cus <= 0) return false;
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     if (m_tiles > FMHA_BALANCED_MAX_ITEMS) return false;

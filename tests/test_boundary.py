@@ -373,6 +373,26 @@ def test_balanced_plan_only_where_the_heaviest_m_tile_outlasts_the_average(b, h,
     assert fmha.workspace_size(p, b, causal) == 0
 
 
+def test_balanced_plan_cache_follows_the_shape():
+    """The launcher keeps the last plan built on a thread; alternating shapes
+    (and compute-unit counts, force, causal) must each get their own plan."""
+    def shape(h, s):
+        p = valid_params(lse=False)
+        p.nhead_q = p.nhead_k = h
+        p.seqlen_q = p.seqlen_k = s
+        return p
+
+    cases = [(shape(2, 40000), 1, 256, False), (shape(1, 32768), 1, 256, False), (shape(2, 40000), 1, 128, False),
+             (shape(2, 3000), 1, 256, True), (shape(2, 3000), 1, 256, False), (shape(2, 40000), 0, 256, True)]
+    first = [fmha.balanced_plan(p, 1, c, cus, f) for p, c, cus, f in cases]
+    assert first[0][0] and first[1][0] and first[3][0] and first[4][0]  # planned
+    assert first[2] == ([], None) and first[5] == ([], None)             # 128 CUs: balanced already; not causal
+    assert first[0] != first[1] and first[3] != first[0]
+    for _ in range(3):
+        for (p, c, cus, f), want in zip(cases, first):
+            assert fmha.balanced_plan(p, 1, c, cus, f) == want
+
+
 def test_ws_entry_rejects_bad_workspaces_and_forms():
     """Refused before anything is launched (no GPU needed)."""
     lib = fmha.load_library()
