@@ -67,18 +67,30 @@ extern "C" hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* p, int batch,
 
 namespace {
 
-// Compute units of the current device (cached per device ordinal).
-int device_cus() {
-    static std::atomic<int> cache[64];
+// What the launch rules read from the current device, cached per device
+// ordinal: compute units, XCDs and each XCD's L2 (MI355X: 256, 8, 4 MiB,
+// also the values used when a query fails).
+struct DeviceShape {
+    int cus, xccs, l2_bytes;
+};
+DeviceShape device_shape() {
+    static std::atomic<int> cache[64][3];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cache[dev].store(n, std::memory_order_relaxed);
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return {256, 8, 4 << 20};
+    int v[3];
+    const hipDeviceAttribute_t attr[3] = {hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeNumberOfXccs,
+                                          hipDeviceAttributeL2CacheSize};
+    const int fallback[3] = {256, 8, 4 << 20};
+    for (int i = 0; i < 3; ++i) {
+        v[i] = cache[dev][i].load(std::memory_order_relaxed);
+        if (v[i] == 0) {
+            if (hipDeviceGetAttribute(&v[i], attr[i], dev) != hipSuccess || v[i] <= 0) v[i] = fallback[i];
+            cache[dev][i].store(v[i], std::memory_order_relaxed);
+        }
     }
-    return n;
+    return {v[0], v[1], v[2]};
 }
+int device_cus() { return device_shape().cus; }
 
 // Form choice from the grid (measured on MI355X, 256 CUs, all forms on one
 // box; blocks = regular-grid blocks, pairs = pair-grid blocks):
@@ -113,17 +125,18 @@ int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_
 // Causal dense grids of more than one batch run on the tile-major entries
 // (grid (nhead_q, batch, tiles): every batch's heaviest M-tiles start first)
 // instead of batch after batch, while the K/V one XCD serves stays within
-// twice an MI355X XCD's 4 MiB L2.  Heads go to the XCDs round robin, so an
-// XCD serves batch x ceil(nhead_k / 8) x seqlen_k x 256 bytes of K/V.  Beyond
-// that the interleaved batches push each sequence's K/V out of L2 before its
-// later M-tiles run.  Measured on causal grids (regular form): +19% B8 H16
-// S1024, +8% B4 H16 S2048, +6% B16 H8 S2048, +2-6% B2 H16 S4096/S8192, and
-// -1 to -5% above 8 MiB.
+// twice its L2 (MI355X: 4 MiB per XCD, 8 XCDs).  Heads go to the XCDs round
+// robin, so an XCD serves batch x ceil(nhead_k / XCDs) x seqlen_k x 256 bytes
+// of K/V.  Beyond that the interleaved batches push each sequence's K/V out
+// of L2 before its later M-tiles run.  Measured on causal grids (regular
+// form): +19% B8 H16 S1024, +8% B4 H16 S2048, +6% B16 H8 S2048, +2-6% B2 H16
+// S4096/S8192, and -1 to -5% above 8 MiB.
 bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     if (!causal || batch < 2 || p->seqstart_q != nullptr) return false;
-    // batch x heads-per-XCD x seqlen_k <= 8 MiB / 256 B, evaluated without overflow
-    const int64_t limit = ((int64_t)8 << 20) / 256;
-    const int64_t rows = (int64_t)batch * (((int64_t)p->nhead_k + 7) / 8);  // <= 2^16 * 2^28
+    const DeviceShape d = device_shape();
+    // batch x heads-per-XCD x seqlen_k <= 2 x L2 / 256 B, evaluated without overflow
+    const int64_t limit = 2 * (int64_t)d.l2_bytes / 256;
+    const int64_t rows = (int64_t)batch * (((int64_t)p->nhead_k + d.xccs - 1) / d.xccs);  // <= 2^16 * 2^31
     return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
