@@ -1,6 +1,6 @@
 """rocprofv3 evidence harness for the FMHA forward kernels (run on the GPU box).
 
-    python -m fmha_native_amd.rocprof --out gpurun_out/prof --summary profiles/NAME.md --json profiles/NAME.json
+    python -m fmha_native_amd.rocprof --out OUT_DIR --summary profiles/NAME.md --json profiles/NAME.json
 
 The gfx950 counterpart of the reference's ATT/counter configuration
 (scripts/rocprof_att.yaml:1-17).  Everything below runs in one process tree
@@ -358,7 +358,7 @@ def profile_short(args):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "prof"))
+    ap.add_argument("--out", default=os.path.join(ROOT, "rocprof_out"))
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
     ap.add_argument("--json", default=None, help="also write the figures bench.py quotes here")
     ap.add_argument("--steps", type=int, default=100)
