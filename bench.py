@@ -320,25 +320,33 @@ def _profile(workload):
         return None
 
 
-def _roofline(achieved, workload):
+def _roofline(achieved, workload, ms_per_step):
     """The roofline object: ``achieved``/``frac`` from this run's HIP events;
     HBM traffic, MFMA busy and the clock from the committed rocprofv3 run of
     the same kernel (one box, one process tree), where
-    frac_from_counters = mfma_busy x clock / 2.4 GHz checks the timer."""
+    frac_from_counters = mfma_busy x clock / 2.4 GHz checks the timer.  The
+    kernel is cycle-bound (the same active cycles per launch on every box
+    measured), so those cycles over this run's time per launch give the clock
+    this box held, which accounts for the difference between the two fracs."""
     prof = _profile(workload)
     r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
          "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
     if prof:
+        active_cycles = prof["clock_ghz"] * prof["counter_dispatch_us"] * 1e3
         r.update({
             "traffic": prof["hbm_bytes_per_launch"],
             "algorithmic_bytes": prof["algorithmic_bytes"],
             "mfma_busy": prof["mfma_busy"],
             "clock_ghz": prof["clock_ghz"],
             "frac_from_counters": prof["frac_from_counters"],
+            "active_cycles_per_launch": round(active_cycles),
+            "clock_ghz_this_run": round(active_cycles / (ms_per_step * 1e6), 4),
             "profile": {"file": os.path.relpath(PROFILE_JSON, ROOT), "kernel": prof["kernel"],
                         "trace_avg_us": prof["trace_avg_us"], "bench_ms_per_step_same_box": prof["bench_ms_per_step"],
-                        "note": "traffic, mfma_busy and clock_ghz come from that run; this line's frac is timed on "
-                                "this box, whose clock under load may differ (frac ~ mfma_busy x clock / 2.4 GHz)"},
+                        "note": "traffic, mfma_busy, clock_ghz and the active cycles (SQ_BUSY_CYCLES per shader "
+                                "engine) come from that run; frac ~ mfma_busy x clock / 2.4 GHz, and this run's "
+                                "frac / frac_from_counters ~ clock_ghz_this_run / clock_ghz (the clock this box "
+                                "held over the profiled one)"},
         })
     return r
 
@@ -446,7 +454,7 @@ def main():
         "data": "synthetic: Q/K/V i.i.d. N(0,1) bf16, seed 42 (fill_normal)",
         "config": {"workload": "dense MHA forward B4 H16 Sq=Sk=2048 D64, no mask, no LSE, BHSD",
                    "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False, "lse": False},
-        "roofline": _roofline(achieved, "cfg2"),
+        "roofline": _roofline(achieved, "cfg2", r2["ms"]),
         "also": {
             "workload": "causal MHA forward B1 H16 Sq=Sk=8192 D64 with LSE (FLOPs x0.5)",
             "ms_per_step": round(r3["ms"], 5),
@@ -454,7 +462,7 @@ def main():
             "pct_bf16_peak": round(100.0 * r3["tflops"] / PEAK_BF16_TFLOPS, 2),
             "reference_protocol": {"ms_per_step": round(r3["ref_ms"], 5), "value": round(r3["ref_tflops"], 2)},
             "form": r3["form"],
-            "roofline": _roofline(r3["tflops"], "cfg3"),
+            "roofline": _roofline(r3["tflops"], "cfg3", r3["ms"]),
             "vs_reference_mi300x": round(r3["tflops"] / 358.1, 3),
         },
         "others": others,
