@@ -326,8 +326,9 @@ def _roofline(achieved, workload, ms_per_step):
     the same kernel (one box, one process tree), where
     frac_from_counters = mfma_busy x clock / 2.4 GHz checks the timer.  The
     kernel is cycle-bound (the same active cycles per launch on every box
-    measured), so those cycles over this run's time per launch give the clock
-    this box held, which accounts for the difference between the two fracs."""
+    measured), so those cycles over a run's time per launch give the clock
+    that box held: this run's frac over the profile run's is the ratio of the
+    two clocks."""
     prof = _profile(workload)
     r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
          "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
@@ -341,12 +342,15 @@ def _roofline(achieved, workload, ms_per_step):
             "frac_from_counters": prof["frac_from_counters"],
             "active_cycles_per_launch": round(active_cycles),
             "clock_ghz_this_run": round(active_cycles / (ms_per_step * 1e6), 4),
+            "clock_ghz_profile_run": round(active_cycles / (prof["bench_ms_per_step"] * 1e6), 4),
+            "frac_profile_run": round(prof["bench_tflops"] / PEAK_BF16_TFLOPS, 4),
             "profile": {"file": os.path.relpath(PROFILE_JSON, ROOT), "kernel": prof["kernel"],
                         "trace_avg_us": prof["trace_avg_us"], "bench_ms_per_step_same_box": prof["bench_ms_per_step"],
-                        "note": "traffic, mfma_busy, clock_ghz and the active cycles (SQ_BUSY_CYCLES per shader "
-                                "engine) come from that run; frac ~ mfma_busy x clock / 2.4 GHz, and this run's "
-                                "frac / frac_from_counters ~ clock_ghz_this_run / clock_ghz (the clock this box "
-                                "held over the profiled one)"},
+                        "note": "traffic, mfma_busy, clock_ghz (a lower bound from the counter pass) and the "
+                                "active cycles (SQ_BUSY_CYCLES per shader engine) come from that run; "
+                                "frac_from_counters = mfma_busy x clock_ghz / 2.4 GHz; the active cycles over each "
+                                "run's own time per launch give the clock each box held (clock_ghz_this_run, "
+                                "clock_ghz_profile_run), and frac / frac_profile_run ~ their ratio"},
         })
     return r
 
