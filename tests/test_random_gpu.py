@@ -6,7 +6,10 @@ Forty shapes drawn over the kernel's parameter space: batch 1-4, kv heads
 or not, BHSD or BSHD storage, or a varlen batch of 1-6 sequences of 1-400
 tokens.  Each runs in every kernel form against the oracle with the
 reference's pass rule and inputs (``fill_random``), as the fixed 63-row
-matrix does; this covers combinations that matrix does not reach.
+matrix does; this covers combinations that matrix does not reach.  A wider
+sweep (400 more shapes, up to 1,500 keys, varlen batches of up to 8
+sequences including empty ones, H up to 32) runs every form, the automatic
+choice and the balanced causal form in one test.
 """
 import numpy as np
 import pytest
@@ -61,3 +64,53 @@ def test_random_shape_matches_oracle(prob, form):
     res = check_problem(prob, dist="ref", seed=7, rule="reference", variant=FORMS[form])
     print(res, flush=True)
     assert res["pass"], res
+
+
+def _draw_wide(i):
+    rng = np.random.default_rng(50000 + i)
+    hk = int(rng.choice([1, 2, 4]))
+    hq = hk * int(rng.choice([1, 2, 4, 8]))
+    causal = bool(rng.integers(0, 2))
+    lse = bool(rng.integers(0, 2))
+    if rng.random() < 0.25:
+        seqs = tuple(int(x) for x in rng.integers(0, 600, int(rng.integers(1, 9))))
+        if sum(seqs) == 0:
+            seqs = (1,) + seqs
+        return Problem(batch=0, nhead_q=hq, nhead_k=hk, seqlen_q=0, causal=causal, lse=lse, varlen_seqs=seqs,
+                       name=f"w{i}-varlen{seqs}")
+    b = int(rng.integers(1, 4))
+    short = rng.random() < 0.3
+    sq = int(rng.integers(1, 129 if short else 1500))
+    sk = int(rng.integers(1, 129 if short else 1500))
+    layout = "bshd" if rng.random() < 0.3 else "bhsd"
+    return Problem(batch=b, nhead_q=hq, nhead_k=hk, seqlen_q=sq, seqlen_k=sk, causal=causal, lse=lse, layout=layout,
+                   name=f"w{i}-b{b}h{hq}k{hk}-s{sq}x{sk}-{'c' if causal else 'd'}")
+
+
+def test_wide_random_sweep():
+    import oracle
+    from oracle import verify
+
+    from harness import make_inputs, run_kernel
+
+    forms = dict(FORMS, auto=fmha.VARIANT_AUTO, balanced=fmha.VARIANT_BALANCED)
+    failed = []
+    runs = 0
+    for i in range(400):
+        prob = _draw_wide(i)
+        q, k, v = make_inputs(prob, "ref", 100 + i)
+        o_ref, lse_ref = oracle.run(prob, q, k, v)
+        for name, var in forms.items():
+            if (name == "persistent" and prob.varlen) or (name == "short" and prob.seqlen_k > 128) or \
+                    (name == "balanced" and (prob.varlen or not prob.causal)):
+                continue
+            ob, lb = run_kernel(prob, q, k, v, variant=var)
+            ok = verify.reference_rule(o_ref, verify.bf16_bits_to_f32(ob))["pass"]
+            if prob.lse:
+                ok = ok and verify.lse_rule(lse_ref, lb)["pass"]
+            runs += 1
+            if not ok:
+                failed.append((prob.name, name))
+        if i % 100 == 99:
+            print(f"wide sweep: {i + 1} shapes, {runs} launches, {len(failed)} failed", flush=True)
+    assert not failed, failed[:20]
