@@ -224,6 +224,31 @@ bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, b
     return true;
 }
 
+// Whether the automatic choice takes a balanced plan: where the balanced form
+// measured faster than the launch without a workspace (split-KV or the
+// regular form; all three on one box, causal, 256 CUs, blocks = regular-grid
+// blocks, heaviest = key tiles of the last M-tile, avg = key tiles per
+// resident block).  It pays for its second launch, the split M-tiles' extra
+// prologues and the partials' traffic only when the M-tiles are long:
+//  * at most one block per CU: heaviest >= 64 (+10-41 % at 4096-8192 keys),
+//    or >= 32 at up to half a block per CU (+16 % B1 H8 S2048); shorter
+//    M-tiles lose 15-50 % (B2-B16 H16 S256-S1024);
+//  * up to 1.5 blocks per CU: heaviest >= 128 (+8.5 % B1 H5 S8192; 64:
+//    -2.5 %);
+//  * 1.5-2 blocks per CU: never (split-KV or regular are 1.4-7 % faster at
+//    4096-32768 keys);
+//  * more: a partial second round whose heaviest M-tile outlasts 1.5x the
+//    average, with heaviest >= 128 (cfg5 B1 H2 S40000 +13 %; +0.5-15 % at
+//    564-672 blocks with 8192-80000 keys; 64: -7 %; at 768 blocks, where the
+//    heaviest is ~1.3x the average, -11 % to +0.7 %).
+bool balanced_pays(int64_t blocks, int heaviest, double avg, int64_t cus) {
+    if (heaviest <= avg) return false;  // the heaviest-first order balances already
+    if (blocks <= cus) return heaviest >= 64 || (2 * blocks <= cus && heaviest >= 32);
+    if (2 * blocks <= 3 * cus) return heaviest >= 128;
+    if (blocks <= 2 * cus) return false;
+    return heaviest >= 128 && heaviest > 1.5 * avg;
+}
+
 bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force,
                          FmhaBalancedArgs* a, int64_t* ws_bytes) {
     if (!causal || p->seqstart_q != nullptr || batch <= 0 || p->seqlen_q <= 0 || cus <= 0) return false;
@@ -234,7 +259,7 @@ bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t 
     total *= (double)p->nhead_q * batch;
     const double avg = total / (2.0 * (double)cus);  // key tiles per resident block
     const int heaviest = causal_ntiles(p, m_tiles - 1);
-    if (!force && heaviest <= avg) return false;
+    if (!force && !balanced_pays((int64_t)m_tiles * p->nhead_q * batch, heaviest, avg, cus)) return false;
     const double limit = std::max(2.0, avg / 2);
     int split_from = m_tiles;  // key tiles grow with the M-tile: the split ones are a suffix
     while (split_from > 0 && causal_ntiles(p, split_from - 1) > limit) --split_from;

@@ -157,7 +157,12 @@ hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int
 /* The launch with a caller-provided workspace (this build's own; no
  * counterpart in the reference).  Dense causal launches whose heaviest M-tile
  * would outlast the average work per resident block (long sequences with few
- * heads, e.g. B1 H2 S40000) run the balanced form: the M-tiles with more key
+ * heads, e.g. B1 H2 S40000) run the balanced form where it measured faster
+ * (M-tiles of >= 64 key tiles on grids of at most one block per compute
+ * unit, >= 128 up to 1.5 blocks per unit or on a partial second round whose
+ * heaviest M-tile outlasts 1.5x the average; never at 1.5-2 blocks per
+ * unit, nor for shorter M-tiles except >= 32 key tiles at up to half a block
+ * per unit): the M-tiles with more key
  * tiles than half that average are split into two key halves, every item is
  * dispatched heaviest first from a table in the kernarg, each half leaves its
  * partial result in the workspace and a second launch merges the halves

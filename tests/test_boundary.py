@@ -373,6 +373,38 @@ def test_balanced_plan_only_where_the_heaviest_m_tile_outlasts_the_average(b, h,
     assert fmha.workspace_size(p, b, causal) == 0
 
 
+@pytest.mark.parametrize("b,h,s,planned", [
+    (1, 2, 40000, True),    # cfg5: 626 blocks, a partial second round of long M-tiles
+    (1, 8, 4096, True),     # 256 blocks (one per CU), 64 key tiles
+    (1, 8, 2048, True),     # 128 blocks (half a block per CU), 32 key tiles
+    (1, 5, 8192, True),     # 320 blocks (1.25 per CU), 128 key tiles
+    (1, 9, 8192, True),     # 576 blocks
+    (1, 1, 32768, True),
+    (8, 16, 256, False),    # 256 blocks of 2-4 key tiles: the merge costs more than it saves
+    (16, 16, 256, False),
+    (8, 16, 512, False),
+    (4, 16, 1024, False),
+    (1, 12, 2048, False),   # 192 blocks, 32 key tiles
+    (1, 16, 2048, False),   # 256 blocks, 32 key tiles
+    (1, 10, 4096, False),   # 320 blocks, 64 key tiles
+    (2, 16, 2048, False),   # 512 blocks (two per CU): split-KV or regular
+    (1, 16, 4096, False),
+    (1, 2, 32768, False),
+    (1, 20, 4096, False),   # 640 blocks, 64 key tiles
+    (1, 6, 16384, False),   # 768 blocks: the heaviest M-tile is ~1.3x the average
+    (1, 16, 8192, False),   # cfg3
+])
+def test_balanced_plan_where_it_measured_faster(b, h, s, planned):
+    """The automatic choice takes a balanced plan only where the balanced form
+    measured faster than the launch without a workspace (256 CUs)."""
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = h
+    p.seqlen_q = p.seqlen_k = s
+    items, _ = fmha.balanced_plan(p, b, 1, 256)
+    assert bool(items) == planned
+    assert fmha.balanced_plan(p, b, 1, 256, True)[0]  # forced: always a plan
+
+
 def test_balanced_plan_cache_follows_the_shape():
     """The launcher keeps the last plan built on a thread; alternating shapes
     (and compute-unit counts, force, causal) must each get their own plan."""
