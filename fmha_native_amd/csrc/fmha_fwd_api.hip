@@ -140,8 +140,12 @@ bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
-// Keys the short form holds at once (two 64-key tiles).
+// Keys the short form's exact path holds at once (two 64-key tiles); longer
+// key ranges take its ring path.
 constexpr int kShortKeys = 2 * FMHA_KN0;
+// Keys up to which the automatic choice takes the ring path: on every grid of
+// two blocks' worth of rows per compute unit, and causal on grids of eight.
+constexpr int kShortRingKeys = 3 * FMHA_KN0, kShortRingKeysCausal = 6 * FMHA_KN0;
 
 // blocks of the regular grid and of the pair grid
 int64_t grid_blocks(const FmhaFwdParams* p, int batch) {
@@ -151,16 +155,27 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
     return (int64_t)p->nhead_q * (((p->seqlen_q + kM0 - 1) / kM0 + 1) / 2) * batch;
 }
 
-// The automatic form of a dense launch: the short form when all keys fit two
-// tiles (seqlen_k is exact there) and the launch has at least two blocks'
-// worth of query rows per compute unit, else the grid-shape rule above.
-// Kernel trace, H16, S64 and S128, B1-B128 (dense and causal): the short form
+// The automatic form of a dense launch: the short form when its keys fit
+// three tiles (seqlen_k is exact there; two tiles: the exact path, three:
+// the ring path) and the launch has at least two blocks' worth of query rows
+// per compute unit, or, causal, up to 384 keys with at least eight; else the
+// grid-shape rule above.
+// Kernel trace, H16, S64 and S128, B1-B128 (dense and causal): the exact path
 // is 9-30 % faster from 65,536 rows up (B32 S128, B64 S64) and up to 13 %
 // slower on smaller grids, where one block's latency sets the launch time
-// (B32 S64, 32,768 rows in 512 half-filled blocks: -3.5 %).
+// (B32 S64, 32,768 rows in 512 half-filled blocks: -3.5 %).  Back to back,
+// H16, 65,536-262,144 rows, against the regular form: the ring path is 8-14 %
+// faster dense at 160-192 keys, 3 % at 224, -6 to +1 % at 256-320, 2-8 %
+// slower at 384; causal 12-21 % faster at 160-192 keys at every size, 7-11 %
+// at 224-384 keys from 262,144 rows and -14 to +2 % below.  Past a few key
+// tiles the regular form's software pipeline (GEMM0 of the next tile beside
+// the softmax of this one) catches up with the ring path's four blocks per
+// compute unit; causal grids keep the ring path longer (their light M-tiles
+// are short).
 int pick_dense(const FmhaFwdParams* p, int batch, int causal, int64_t cus) {
     const int64_t rows = (int64_t)batch * p->nhead_q * p->seqlen_q;
-    if (p->seqlen_k <= kShortKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
+    if (p->seqlen_k <= kShortRingKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
+    if (causal && p->seqlen_k <= kShortRingKeysCausal && rows >= 8 * cus * kM0) return FMHA_VARIANT_SHORT;
     return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
 }
 
@@ -372,7 +387,6 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
         return hipErrorInvalidValue;  // the balanced form needs fmha_fwd_d64_bf16_ws
     const bool varlen = p->seqstart_q != nullptr;
     if (variant == FMHA_VARIANT_PERSISTENT && varlen) return hipErrorInvalidValue;  // dense only
-    if (variant == FMHA_VARIANT_SHORT && p->seqlen_k > kShortKeys) return hipErrorInvalidValue;
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
@@ -400,18 +414,15 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
         variant = varlen ? pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus())
                          : pick_dense(p, batch, causal, device_cus());
     if (variant == FMHA_VARIANT_SHORT) {
-        const dim3 block(kBlockSize);
-        if (varlen) {
-            if (causal)
-                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk1_varlen, grid, block, 0, stream, *p);
-            else
-                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk0_varlen, grid, block, 0, stream, *p);
-        } else {
-            if (causal)
-                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk1, grid, block, 0, stream, *p);
-            else
-                hipLaunchKernelGGL(fmha_fwd_d64_bf16_short_msk0, grid, block, 0, stream, *p);
-        }
+        // the exact path when seqlen_k (every sequence's bound) fits two tiles
+        using Entry = void (*)(FmhaFwdParams);
+        static const Entry entries[2][2][2] = {
+            {{fmha_fwd_d64_bf16_short_msk0, fmha_fwd_d64_bf16_short_msk0_varlen},
+             {fmha_fwd_d64_bf16_short_msk1, fmha_fwd_d64_bf16_short_msk1_varlen}},
+            {{fmha_fwd_d64_bf16_short_ring_msk0, fmha_fwd_d64_bf16_short_ring_msk0_varlen},
+             {fmha_fwd_d64_bf16_short_ring_msk1, fmha_fwd_d64_bf16_short_ring_msk1_varlen}}};
+        const Entry e = entries[p->seqlen_k > kShortKeys ? 1 : 0][causal ? 1 : 0][varlen ? 1 : 0];
+        hipLaunchKernelGGL(e, grid, dim3(kBlockSize), 0, stream, *p);
         return hipGetLastError();
     }
     if (tile_major) {  // causal, dense, batch > 1

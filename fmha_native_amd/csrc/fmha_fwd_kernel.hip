@@ -1270,8 +1270,21 @@ constexpr int kShortTiles = 2;
 // not read again by this launch (2.5 % faster on dense B128 H16 S128).
 constexpr int kStoreStream = 2;
 
-template <bool kCausal, bool kVarlen>
-__device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, int mt, lds_char* kl, lds_char* vl) {
+// The ring path of the short form (longer key ranges, up to 512 keys by the
+// launcher's rule): K and V tiles in two-stage rings (32 KiB of LDS, each
+// stage its own __shared__ array, as the regular form's rings), prefetched
+// one tile ahead; one 64-key tile per iteration whose two 32-key halves each
+// take GEMM0, an online softmax with the exact running row max and their
+// share of GEMM1 (half a tile of scores at a time keeps the wave within 128
+// VGPRs).
+// The exact path holds its two tiles in the same four arrays.
+struct ShortLds {
+    lds_char* k[2];
+    lds_char* v[2];
+};
+
+template <bool kCausal, bool kVarlen, bool kRingPath>
+__device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, int mt, const ShortLds& lds) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31;
@@ -1315,32 +1328,30 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
         const int e = last + shift + 1;
         kv_end = e < 0 ? 0 : (e > sk ? sk : e);
     }
-    const int ntiles = (kv_end + kTileN - 1) / kTileN;  // <= 2 (the launcher's rule)
-    // A varlen sequence with more keys than the form holds breaks the caller's
-    // promise (seqlen_k bounds every sequence): its rows get NaN in O and LSE
-    // instead of a softmax over its first 128 keys.
-    const bool too_long = kVarlen && ntiles > kShortTiles;
+    const int ntiles = (kv_end + kTileN - 1) / kTileN;  // exact path: <= 2 (the launcher's rule)
+    // A varlen sequence with more keys than the exact path holds breaks the
+    // caller's promise (seqlen_k bounds every sequence): its rows get NaN in O
+    // and LSE instead of a softmax over its first 128 keys.  The ring path
+    // takes any number of keys.
+    const bool too_long = !kRingPath && kVarlen && ntiles > kShortTiles;
     const int wrow0 = row0 + wave * kRowsPerWave;
     const int my_row = wrow0 + l32;
-
-    // K rows into LDS, Q rows into registers, then V rows into LDS (the ring's
-    // layout and swizzles: tile t at t * 8 KiB, each wave 2 x 1 KiB of each
-    // tile; rows past the keys read as zero).  The scores wait only for K and
-    // Q (vmcnt counts the four V loads still in flight), GEMM1 for V.
     const int ld_row = 2 * wave * 8 + (lane >> 3);
     const int ld_pc = lane & 7;
+    const int fk = k_swz(l32);
+    const int lim = kCausal ? min(sk - 1, my_row + shift) : sk - 1;
+    const float ninf = in_vgpr(-__builtin_inff());
+    const float scale = p.scale;
+    const float scale_v = in_vgpr(scale);
+    const int g = lane >> 4, i16 = lane & 15, e4 = i16 >> 2, c4 = i16 & 3;
+    float m_ref, l_part = 0.0f;
+    f32x16 oacc[2];
 #pragma unroll
-    for (int t = 0; t < kShortTiles; ++t) {
-        const uint32_t tk = (uint32_t)t * kTileN * p.stride_k * 2;
-        const auto rk = make_rsrc((const char*)kbase + tk, t < ntiles ? kbytes - tk : 0u);
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = ld_row + 8 * i;
-            lds_dma_16(rk, kl + t * kTileBytes + (2 * wave + i) * 1024, row * p.stride_k * 2 + ((ld_pc ^ k_swz(row)) << 4));
-        }
-    }
+        for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
     bf16x8 qop[4];
-    {
+    auto load_q = [&]() {
         const auto rq = make_rsrc(qbase, qbytes);
         const int qoff = my_row * p.stride_q * 2 + hi * 16;
 #pragma unroll
@@ -1348,95 +1359,203 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
             i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
             qop[t] = __builtin_bit_cast(bf16x8, raw);
         }
-    }
+    };
+    // K (V) tile t into the LDS stage at `st`: the ring's layout and
+    // swizzles, each wave 2 x 1 KiB of the tile; rows past the keys (and
+    // tiles past ntiles) read as zero
+    auto issue_k = [&](int t, lds_char* st) {
+        const uint32_t tk = (uint32_t)t * kTileN * p.stride_k * 2;
+        const auto rk = make_rsrc((const char*)kbase + tk, t < ntiles ? kbytes - tk : 0u);
 #pragma unroll
-    for (int t = 0; t < kShortTiles; ++t) {
+        for (int i = 0; i < 2; ++i) {
+            const int row = ld_row + 8 * i;
+            lds_dma_16(rk, st + (2 * wave + i) * 1024, row * p.stride_k * 2 + ((ld_pc ^ k_swz(row)) << 4));
+        }
+    };
+    auto issue_v = [&](int t, lds_char* st) {
         const uint32_t tv = (uint32_t)t * kTileN * p.stride_v * 2;
         const auto rv = make_rsrc((const char*)vbase + tv, t < ntiles ? vbytes - tv : 0u);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int row = ld_row + 8 * i;
-            lds_dma_16(rv, vl + t * kTileBytes + (2 * wave + i) * 1024, row * p.stride_v * 2 + ((ld_pc ^ v_swz(row)) << 4));
+            lds_dma_16(rv, st + (2 * wave + i) * 1024, row * p.stride_v * 2 + ((ld_pc ^ v_swz(row)) << 4));
         }
+    };
+    // per-lane LDS read offsets inside a tile (the regular form's): K rows
+    // kb*32 + l32, logical chunk 2k + hi; V^T through ds_read_b64_tr_b16
+    uint32_t k_rd[4], v_rd[2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) k_rd[k] = l32 * kRowBytes + (((2 * k + hi) ^ fk) << 4);
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+        const int row = 4 * hi + e4;
+        const int chunk = 4 * db + 2 * (g & 1) + (c4 >> 1);
+        v_rd[db] = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c4 & 1) * 8;
     }
-    vmcnt_wait<2 * kShortTiles>();
-    ring_barrier();
+    // GEMM0 of 32 keys (kb: which half of the LDS tile kt) into s
+    auto gemm0_half = [&](const lds_char* kt, int kb, f32x16& s) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s = mfma(lds_read_b128(kt + k_rd[k] + kb * 32 * kRowBytes), qop[k], s);
+    };
+    // GEMM1 of 32 keys (kb: which half of the LDS tile vt) with their P^T
+    auto gemm1_half = [&](const lds_char* vt, int kb, const bf16x8* pp) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+                oacc[db] = mfma(lds_read_vt(vt + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[k], oacc[db]);
+    };
 
-    const int fk = k_swz(l32);
-    f32x16 sacc[kShortTiles][2];
+    if constexpr (!kRingPath) {
+        // K rows into LDS, Q rows into registers, then V rows into LDS (tile t
+        // at t * 8 KiB).  The scores wait only for K and Q (vmcnt counts the four
+        // V loads still in flight), GEMM1 for V.
 #pragma unroll
-    for (int t = 0; t < kShortTiles; ++t)
+        for (int t = 0; t < kShortTiles; ++t) issue_k(t, lds.k[t]);
+        load_q();
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x16 acc = {};
-            if (t < ntiles) {
+        for (int t = 0; t < kShortTiles; ++t) issue_v(t, lds.v[t]);
+        vmcnt_wait<2 * kShortTiles>();
+        ring_barrier();
+
+        f32x16 sacc[kShortTiles][2];
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    acc = mfma(lds_read_b128(kl + t * kTileBytes + (kb * 32 + l32) * kRowBytes + (((2 * k + hi) ^ fk) << 4)),
-                               qop[k], acc);
+        for (int t = 0; t < kShortTiles; ++t)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                f32x16 acc = {};
+                if (t < ntiles) gemm0_half(lds.k[t], kb, acc);
+                sacc[t][kb] = acc;
             }
-            sacc[t][kb] = acc;
-        }
-    // mask (keys >= sk, causal keys > row + shift, and the tiles past ntiles),
-    // then the exact row max over both tiles
-    const int lim = kCausal ? min(sk - 1, my_row + shift) : sk - 1;
-    const float ninf = in_vgpr(-__builtin_inff());
-    float mx = ninf;
+        // mask (keys >= sk, causal keys > row + shift, and the tiles past ntiles),
+        // then the exact row max over both tiles
+        float mx = ninf;
 #pragma unroll
-    for (int t = 0; t < kShortTiles; ++t) {
-        const int d = lim - (t * kTileN + 4 * hi);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
-                sacc[t][kb][r] = (c <= d && t < ntiles) ? sacc[t][kb][r] : ninf;
-                mx = fmaxf(mx, sacc[t][kb][r]);
-            }
-    }
-    const float scale = p.scale;
-    const float scale_v = in_vgpr(scale);
-    const float m_ref = fmaxf(kMaxSeed, wave_max_halves(mx) * scale);  // -FLT_MAX for a row with no key
-    const float neg_ms = -m_ref;
-    float l_part = 0.0f;
-    f32x16 oacc[2];
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
-    vmcnt_wait<0>();  // V
-    ring_barrier();
-    const int g = lane >> 4, i16 = lane & 15, e4 = i16 >> 2, c4 = i16 & 3;
-#pragma unroll
-    for (int t = 0; t < kShortTiles; ++t) {
-        if (t < ntiles) {
-            bf16x8 pp[4];
+        for (int t = 0; t < kShortTiles; ++t) {
+            const int d = lim - (t * kTileN + 4 * hi);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    bf16x8 pk;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][kb][8 * k + e], scale_v, neg_ms));
-                        l_part += pv;
-                        pk[e] = (__bf16)pv;
-                    }
-                    pp[2 * kb + k] = pk;
+                for (int r = 0; r < 16; ++r) {
+                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                    sacc[t][kb][r] = (c <= d && t < ntiles) ? sacc[t][kb][r] : ninf;
+                    mx = fmaxf(mx, sacc[t][kb][r]);
                 }
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int k = 0; k < 2; ++k)
-#pragma unroll
-                    for (int db = 0; db < 2; ++db) {
-                        const int row = 4 * hi + e4;
-                        const int chunk = 4 * db + 2 * (g & 1) + (c4 >> 1);
-                        const uint32_t vrd = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c4 & 1) * 8;
-                        oacc[db] = mfma(lds_read_vt(vl + t * kTileBytes + vrd + (kb * 32 + 16 * k) * kRowBytes),
-                                        pp[2 * kb + k], oacc[db]);
-                    }
         }
+        m_ref = fmaxf(kMaxSeed, wave_max_halves(mx) * scale);  // -FLT_MAX for a row with no key
+        const float neg_ms = -m_ref;
+        vmcnt_wait<0>();  // V
+        ring_barrier();
+#pragma unroll
+        for (int t = 0; t < kShortTiles; ++t) {
+            if (t < ntiles) {
+                bf16x8 pp[4];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        bf16x8 pk;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][kb][8 * k + e], scale_v, neg_ms));
+                            l_part += pv;
+                            pk[e] = (__bf16)pv;
+                        }
+                        pp[2 * kb + k] = pk;
+                    }
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) gemm1_half(lds.v[t], kb, pp + 2 * kb);
+            }
+        }
+    } else {
+        // prologue: K(0), Q, V(0).  Iteration t (stage J = t % 2) waits for
+        // K(t), V(t) (and Q), then prefetches tile t+1 into the other stage,
+        // which tile t-1 used (every wave is past it after the barrier), and
+        // computes tile t while those loads fly.
+        issue_k(0, lds.k[0]);
+        load_q();
+        issue_v(0, lds.v[0]);
+        m_ref = kMaxSeed;
+        // scores of one 32-key half: GEMM0, then the mask (keys >= sk, causal
+        // keys > row + shift) where the half reaches past it
+        auto scores = [&](const lds_char* kt, int t, int kb, f32x16& s) {
+            s = f32x16{};
+            gemm0_half(kt, kb, s);
+            const int d = lim - (t * kTileN + 32 * kb + 4 * hi);
+            if (__builtin_amdgcn_ballot_w64(d < 31)) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int c = 8 * (r >> 2) + (r & 3);
+                    s[r] = c <= d ? s[r] : ninf;
+                }
+            }
+        };
+        // exact max of the half's rows, scaled (-inf for a row with no key)
+        auto half_max = [&](const f32x16& s) {
+            float mx = ninf;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            return wave_max_halves(mx) * scale;
+        };
+        // P = exp2(s*scale - m_ref), bf16-packed, and this lane's sum of P
+        // (fp32, before the rounding)
+        auto exp_half = [&](const f32x16& s, bf16x8* pp) {
+            const float neg_ms = -m_ref;
+            float ls[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                bf16x8 pk;
+                float acc;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * k + e], scale_v, neg_ms));
+                    acc = e == 0 ? pv : acc + pv;
+                    pk[e] = (__bf16)pv;
+                }
+                ls[k] = acc;
+                pp[k] = pk;
+            }
+            return ls[0] + ls[1];
+        };
+        // online softmax with the exact running row max of each half; O^T and
+        // l move to a new max only where it grew (always at a row's first
+        // visible keys, rarely after).  The regular form's speculative frame
+        // would save the max but needs the scores and P live together on its
+        // re-framing path, past 128 VGPRs.
+        auto iteration = [&](int t, auto stage_c) {
+            constexpr int J = decltype(stage_c)::value;
+            vmcnt_wait<0>();
+            ring_barrier();
+            issue_k(t + 1, lds.k[J ^ 1]);
+            issue_v(t + 1, lds.v[J ^ 1]);
+            lds_char* const kt = lds.k[J];
+            lds_char* const vt = lds.v[J];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                __builtin_amdgcn_sched_barrier(0);
+                f32x16 sacc;
+                scores(kt, t, kb, sacc);
+                const float m_new = fmaxf(m_ref, half_max(sacc));
+                if (__builtin_amdgcn_ballot_w64(m_new > m_ref)) {
+                    const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+#pragma unroll
+                    for (int db = 0; db < 2; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+                    l_part *= alpha;
+                    m_ref = m_new;
+                }
+                bf16x8 pp[2];
+                l_part += exp_half(sacc, pp);
+                __builtin_amdgcn_sched_barrier(0);
+                gemm1_half(vt, kb, pp);
+            }
+        };
+        for (int t = 0; t < ntiles; t += 2) {
+            iteration(t, std::integral_constant<int, 0>{});
+            if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{});
+        }
+        vmcnt_wait<0>();  // the last iteration's (empty) refills
     }
 
     // epilogue: O = O^T / l through this wave's rows of the K tile area (every
@@ -1444,7 +1563,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
     const float l_tot = wave_sum_halves(l_part);
     const float inv = too_long ? __builtin_nanf("") : l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     ring_barrier();
-    lds_char* const tb = kl + wave * (kRowsPerWave * kRowBytes);
+    lds_char* const tb = (wave < 2 ? lds.k[0] : lds.k[1]) + (wave & 1) * (kRowsPerWave * kRowBytes);
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -1703,26 +1822,28 @@ __global__ __launch_bounds__(FMHA_KBLOCK) void fmha_fwd_d64_bf16_balanced_merge(
 }
 
 // ---- short entries (this build's own; no counterpart in the reference):
-// the regular grid for seqlen_k <= 128 (per sequence); 32 KiB of LDS and
-// <= 128 VGPRs, four blocks per compute unit.  Causal entries run the
-// heaviest M-tiles first, as the regular ones. ----
+// the regular grid, <= 128 VGPRs, four blocks per
+// compute unit, 32 KiB of LDS.  The exact entries take seqlen_k <= 128 (per
+// sequence), the ring entries any key count (the launcher's rule: up to 512).
+// Causal entries run the heaviest M-tiles first, as the regular ones. ----
 #define FMHA_SHORT_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
-#define FMHA_SHORT_LDS                                                                                      \
-    __shared__ __attribute__((aligned(1024))) char kl[kShortTiles * kTileBytes];                           \
-    __shared__ __attribute__((aligned(1024))) char vl[kShortTiles * kTileBytes];
-FMHA_SHORT_ATTRS void fmha_fwd_d64_bf16_short_msk0(FmhaFwdParams params) {
-    FMHA_SHORT_LDS
-    fwd_short<false, false>(params, blockIdx.z, blockIdx.x, blockIdx.y, (lds_char*)kl, (lds_char*)vl);
-}
-FMHA_SHORT_ATTRS void fmha_fwd_d64_bf16_short_msk1(FmhaFwdParams params) {
-    FMHA_SHORT_LDS
-    fwd_short<true, false>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, (lds_char*)kl, (lds_char*)vl);
-}
-FMHA_SHORT_ATTRS void fmha_fwd_d64_bf16_short_msk0_varlen(FmhaFwdParams params) {
-    FMHA_SHORT_LDS
-    fwd_short<false, true>(params, blockIdx.z, blockIdx.x, blockIdx.y, (lds_char*)kl, (lds_char*)vl);
-}
-FMHA_SHORT_ATTRS void fmha_fwd_d64_bf16_short_msk1_varlen(FmhaFwdParams params) {
-    FMHA_SHORT_LDS
-    fwd_short<true, true>(params, blockIdx.z, blockIdx.x, gridDim.y - 1 - blockIdx.y, (lds_char*)kl, (lds_char*)vl);
-}
+// every K and V stage its own array
+#define FMHA_SHORT_LDS                                                                                     \
+    __shared__ __attribute__((aligned(1024))) char k0[kTileBytes], k1[kTileBytes], v0[kTileBytes], v1[kTileBytes]; \
+    const ShortLds lds{{(lds_char*)k0, (lds_char*)k1}, {(lds_char*)v0, (lds_char*)v1}};
+#define FMHA_SHORT_ENTRY(name, causal, varlen, ring)                                                       \
+    FMHA_SHORT_ATTRS void name(FmhaFwdParams params) {                                                     \
+        FMHA_SHORT_LDS                                                                                      \
+        fwd_short<causal, varlen, FMHA_SHORT_IS_##ring>(params, blockIdx.z, blockIdx.x,                      \
+                                                        causal ? gridDim.y - 1 - blockIdx.y : blockIdx.y, lds); \
+    }
+#define FMHA_SHORT_IS_EXACT false
+#define FMHA_SHORT_IS_RING true
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0, false, false, EXACT)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1, true, false, EXACT)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0_varlen, false, true, EXACT)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1_varlen, true, true, EXACT)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk0, false, false, RING)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk1, true, false, RING)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk0_varlen, false, true, RING)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk1_varlen, true, true, RING)

@@ -29,7 +29,8 @@ REFERENCE_OFFSETS = {
 KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_d64_bf16_msk0_varlen",
                   "fmha_fwd_d64_bf16_msk1_varlen"]
 SPLIT_ENTRIES = [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("splitkv", "pair") for m in (0, 1)
-                 for v in ("", "_varlen")] + [f"fmha_fwd_d64_bf16_{f}msk1_tilemajor" for f in ("", "splitkv_", "pair_")]
+                 for v in ("", "_varlen")] + [f"fmha_fwd_d64_bf16_{f}msk1_tilemajor" for f in ("", "splitkv_", "pair_")] \
+    + [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("short", "short_ring") for m in (0, 1) for v in ("", "_varlen")]
 
 
 def header_c_functions():
@@ -217,21 +218,24 @@ R, S, P = fmha.VARIANT_REGULAR, fmha.VARIANT_SPLITKV, fmha.VARIANT_PAIR
 
 
 def test_short_form_rule():
-    """Dense launches whose keys fit two 64-key tiles take the short form
+    """Dense launches whose keys fit three 64-key tiles take the short form
     (their seqlen_k is exact) once they hold two blocks' worth of query rows
-    per compute unit (2 x CUs x 128 rows); smaller grids and varlen ones keep
-    the grid-shape rule (a varlen seqlen_k is only a bound the caller gives);
-    an explicit short launch with more keys is refused."""
+    per compute unit (2 x CUs x 128 rows), causal ones with up to 384 keys
+    once they hold eight; smaller grids and varlen ones keep the grid-shape
+    rule (a varlen seqlen_k is only a bound the caller gives)."""
     # valid_params: 4 heads x 128 query rows per batch -> 512 rows
-    for sk, batch, cus, short in ((1, 128, 256, True), (64, 128, 256, True), (128, 128, 256, True),
-                                  (128, 127, 256, False), (129, 128, 256, False), (128, 152, 304, True),
-                                  (128, 151, 304, False), (128, 4096, 256, True)):
-        for causal in (0, 1):
+    for sk, batch, cus, dense, causal_short in (
+            (1, 128, 256, True, True), (64, 128, 256, True, True), (128, 128, 256, True, True),
+            (128, 127, 256, False, False), (128, 152, 304, True, True), (128, 151, 304, False, False),
+            (128, 4096, 256, True, True),
+            (129, 128, 256, True, True), (192, 128, 256, True, True), (192, 127, 256, False, False),
+            (193, 511, 256, False, False), (193, 512, 256, False, True), (384, 512, 256, False, True),
+            (384, 607, 304, False, False), (384, 608, 304, False, True), (385, 4096, 256, False, False),
+            (513, 4096, 256, False, False), (2048, 4096, 256, False, False)):
+        for causal, short in ((0, dense), (1, causal_short)):
             got = fmha.pick_variant(_mut(seqlen_k=sk, lse=None), batch, causal, cus)
             assert (got == fmha.VARIANT_SHORT) if short else (got in (R, S, P)), (sk, batch, cus, causal, got)
     assert fmha.pick_variant(valid_params(varlen=True, lse=False), 4096, 1, 256) in (R, S, P)
-    lib = fmha.load_library()
-    assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(_mut(seqlen_k=129)), 1, 0, fmha.VARIANT_SHORT, None) == INVALID
 
 
 @pytest.mark.parametrize("batch,heads,seqlen,causal,cus,form", [
@@ -291,7 +295,7 @@ def test_rules_at_extreme_counts():
     big = 2**31 - 1
     p = valid_params(lse=False)
     p.nhead_q = p.nhead_k = big
-    p.seqlen_k = 256  # past the short form's 128 keys
+    p.seqlen_k = 600  # past the short form's 384 keys
     assert fmha.tile_major(p, 65535, 1) == 0
     assert fmha.pick_variant(p, 65535, 1, 256) == R
     q = valid_params(lse=False)

@@ -6,8 +6,9 @@ s_barrier of every entry, the wave has no LDS read in flight (an
 ``s_waitcnt lgkmcnt(0)`` follows the last ds_read).  A read left in flight
 would race with the other waves' DMA refill of its stage right after the
 barrier.  Also: no entry spills to scratch, and every entry keeps two waves
-per SIMD (the short form four).  The short form's first wait counts on the
-order its loads are issued in (K, Q, V), which is checked too.
+per SIMD (the short form four).  The short form's first waits count on the
+order its loads are issued in (exact entries: K, Q, V; ring entries: K(0),
+Q, V(0), K(1)), which is checked too.
 """
 import os
 import re
@@ -52,9 +53,10 @@ def test_every_entry_compiled(asm):
         assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
     for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_merge"):
         assert any(e in n for n in names), e
-    for m in (0, 1):
-        for v in ("", "_varlen"):
-            assert any(f"fmha_fwd_d64_bf16_short_msk{m}{v}13FmhaFwdParams" in n for n in names), (m, v)
+    for form in ("short_", "short_ring_"):
+        for m in (0, 1):
+            for v in ("", "_varlen"):
+                assert any(f"fmha_fwd_d64_bf16_{form}msk{m}{v}13FmhaFwdParams" in n for n in names), (form, m, v)
 
 
 def test_no_lds_read_in_flight_at_barriers(asm):
@@ -109,3 +111,49 @@ def test_short_form_issue_order_and_occupancy(asm):
             elif ins.startswith("s_waitcnt") and "vmcnt" in ins:
                 seq.append(re.search(r"vmcnt\((\d+)\)", ins).group(0))
         assert seq == ["L"] * 4 + ["R"] * 4 + ["L"] * 4 + ["vmcnt(4)"], (name, seq)
+
+
+def _lds_bytes(src):
+    """LDS bytes per workgroup of every function from its kernel-info block."""
+    lds = {}
+    for m in re.finditer(r"^\s*\.set\s+(_Z[^.\s]+)\.has_indirect_call.*?; LDSByteSize: (\d+)", src, re.M | re.S):
+        lds[m.group(1)] = int(m.group(2))
+    return lds
+
+
+def test_short_ring_prefetch_is_not_waited_on(asm):
+    """The ring entries prefetch tile t+1 right after the barrier of tile t
+    and wait for it (vmcnt(0)) only before the next barrier.  Their stages
+    are distinct LDS arrays, so the compiler can tell that the prefetch does
+    not alias the reads of tile t; had it inserted a wait that covers the
+    prefetch before those reads, every tile would wait for the next one's
+    loads.  So a vmcnt wait that precedes an LDS read (with no barrier in
+    between) must allow every load issued since the last barrier to stay in
+    flight (the compiler adds such waits for the Q registers: it does not
+    see the hand-written vmcnt(0) before the barrier).  The prologue issues
+    K(0) and V(0) into LDS and Q into registers (two, two and four loads per
+    wave) before the first barrier.  32 KiB of LDS and <= 128 VGPRs keep
+    four blocks per compute unit."""
+    occ, lds = _occupancy(asm), _lds_bytes(asm)
+    rings = {n: b for n, b in _functions(asm).items() if "_short_ring_msk" in n}
+    assert len(rings) == 4
+    for name, body in rings.items():
+        assert occ.get(name) == 4, (name, occ.get(name))
+        assert lds.get(name) == 32 * 1024, (name, lds.get(name))
+        ins = [ln.strip() for ln in body.splitlines() if ln.strip() and not ln.strip().startswith((";", "."))]
+        first = next(i for i, x in enumerate(ins) if x.startswith("s_barrier"))
+        loads = [x for x in ins[:first] if x.startswith("buffer_load_dwordx4")]
+        assert sorted("L" if x.endswith(" lds") else "R" for x in loads) == ["L"] * 4 + ["R"] * 4, (name, loads)
+        since_barrier, checked = None, 0
+        for i, x in enumerate(ins):
+            if x.startswith("s_barrier"):
+                since_barrier = 0
+            elif x.startswith("buffer_load_dwordx4") and since_barrier is not None:
+                since_barrier += 1
+            elif x.startswith("s_waitcnt") and "vmcnt" in x and since_barrier is not None:
+                nxt = next((y for y in ins[i + 1:] if y.startswith(("s_barrier", "ds_read"))), "s_barrier")
+                if nxt.startswith("ds_read"):
+                    n = int(re.search(r"vmcnt\((\d+)\)", x).group(1))
+                    assert n >= since_barrier, (name, i, x, since_barrier)
+                    checked += 1
+        assert checked >= 1, name

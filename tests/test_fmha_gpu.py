@@ -50,8 +50,6 @@ def _dense_only(form, prob):
         pytest.skip("the persistent form takes dense problems only")
     if form == "balanced" and (prob.varlen or not prob.causal):
         pytest.skip("the balanced form takes causal dense problems only")
-    if form == "short" and prob.seqlen_k > 128:
-        pytest.skip("the short form takes at most 128 keys")
 
 
 @pytest.mark.parametrize("form", list(MATRIX_FORMS))
@@ -498,6 +496,41 @@ def test_short_varlen_flags_a_sequence_longer_than_the_bound(causal):
     ok = ~flagged
     assert np.all(np.abs(o[:, ok] - o_ref[:, ok]) <= 1e-2 + 1e-2 * np.abs(o_ref[:, ok]))
     assert np.abs(lse[:, ok] - lse_ref[:, ok]).max() <= 1e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_short_ring_varlen_takes_any_key_count(causal):
+    """Past 128 keys the short form runs its ring entries, which stream any
+    number of key tiles: varlen sequences of 1 to 1,100 keys in one launch
+    match the oracle."""
+    seqs = (1, 64, 129, 300, 511, 700, 1100, 5)
+    p = Problem(batch=0, nhead_q=4, nhead_k=2, seqlen_q=0, causal=causal, lse=True, varlen_seqs=seqs)
+    print("launch: short ring varlen", seqs, "causal", causal, flush=True)
+    res = _report(check_problem(p, dist="ref", seed=11, rule="reference", variant=fmha.VARIANT_SHORT))
+    assert res["pass"], res
+
+
+@pytest.mark.parametrize("sq,sk", [(2000, 2000), (700, 1500), (1500, 700)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_short_ring_equals_regular_on_long_rows(causal, sq, sk):
+    """Dense B2 H3, up to 32 key tiles per block (odd and even ring stages,
+    a partial last tile, more keys than queries and the reverse): the ring
+    entries agree with the regular form to the bf16 rounding of O and the
+    fp32 rounding of LSE, with inputs scaled x4 so that row maxima keep
+    growing along the keys (the online rescale runs on many tiles)."""
+    p = Problem(batch=2, nhead_q=3, nhead_k=3, seqlen_q=sq, seqlen_k=sk, causal=causal, lse=True)
+    q, k, v = make_inputs(p, "normal", 21, 4.0)
+    o_s, l_s = run_kernel(p, q, k, v, variant=fmha.VARIANT_SHORT)
+    o_r, l_r = run_kernel(p, q, k, v, variant=fmha.VARIANT_REGULAR)
+    print("short ring vs regular", (sq, sk), "causal", causal, flush=True)
+    a, b = verify.bf16_bits_to_f32(o_s), verify.bf16_bits_to_f32(o_r)
+    # P is rounded to bf16 in different frames (exact running max against
+    # the regular form's speculative one): a few bf16 ulps of O apart
+    rms = float(np.sqrt(np.mean(b * b)))
+    assert np.all(np.abs(a - b) <= 2e-2 * np.abs(b) + 1e-2 * rms), np.abs(a - b).max()
+    empty = np.isinf(l_r)  # causal rows with no visible key: LSE -inf in both, O 0
+    assert np.array_equal(l_s[empty], l_r[empty]) and np.all(a.reshape(-1, 64)[empty] == 0)
+    assert np.abs(l_s[~empty] - l_r[~empty]).max() <= 1e-4
 
 
 @pytest.mark.parametrize("causal", [False, True])
