@@ -5,10 +5,10 @@ property it relies on is checked on the generated code itself: at every
 s_barrier of every entry, the wave has no LDS read in flight (an
 ``s_waitcnt lgkmcnt(0)`` follows the last ds_read).  A read left in flight
 would race with the other waves' DMA refill of its stage right after the
-barrier.  Also: no entry spills to scratch, and every entry keeps two waves
-per SIMD (the short form four).  The short form's first waits count on the
-order its loads are issued in (exact entries: K, Q, V; ring entries: K(0),
-Q, V(0), K(1)), which is checked too.
+barrier.  Also: no entry spills to scratch, every entry keeps two waves per
+SIMD (the short form four), no compiler-inserted wait holds a tile's reads
+until the next tile's prefetch lands, and the short form's exact entries
+issue their loads in the order their first wait counts on (K, Q, V).
 """
 import os
 import re
@@ -121,19 +121,44 @@ def _lds_bytes(src):
     return lds
 
 
-def test_short_ring_prefetch_is_not_waited_on(asm):
-    """The ring entries prefetch tile t+1 right after the barrier of tile t
-    and wait for it (vmcnt(0)) only before the next barrier.  Their stages
-    are distinct LDS arrays, so the compiler can tell that the prefetch does
-    not alias the reads of tile t; had it inserted a wait that covers the
-    prefetch before those reads, every tile would wait for the next one's
-    loads.  So a vmcnt wait that precedes an LDS read (with no barrier in
-    between) must allow every load issued since the last barrier to stay in
-    flight (the compiler adds such waits for the Q registers: it does not
-    see the hand-written vmcnt(0) before the barrier).  The prologue issues
-    K(0) and V(0) into LDS and Q into registers (two, two and four loads per
-    wave) before the first barrier.  32 KiB of LDS and <= 128 VGPRs keep
-    four blocks per compute unit."""
+def _prefetch_waits(body):
+    """(wait, loads issued since the last barrier) for every vmcnt wait that
+    precedes an LDS read with no barrier in between."""
+    ins = [ln.strip() for ln in body.splitlines() if ln.strip() and not ln.strip().startswith((";", "."))]
+    since, out = None, []
+    for i, x in enumerate(ins):
+        if x.startswith("s_barrier"):
+            since = 0
+        elif x.startswith("buffer_load") and since is not None:
+            since += 1
+        elif x.startswith("s_waitcnt") and "vmcnt" in x and since is not None:
+            nxt = next((y for y in ins[i + 1:] if y.startswith(("s_barrier", "ds_read"))), "s_barrier")
+            if nxt.startswith("ds_read"):
+                out.append((int(re.search(r"vmcnt\((\d+)\)", x).group(1)), since))
+    return out
+
+
+def test_no_wait_covers_a_prefetch(asm):
+    """Every entry prefetches K/V tiles by LDS-DMA right after a barrier and
+    waits for them only before a later barrier.  Its ring stages are distinct
+    LDS arrays indexed by compile-time stage numbers, so the compiler can
+    tell that a prefetch does not alias the reads of the current tile; had it
+    inserted a wait covering the prefetch before those reads, every tile
+    would wait for the next one's loads.  So a vmcnt wait that precedes an
+    LDS read (no barrier in between) must let every load issued since the
+    last barrier stay in flight (the compiler adds such waits for register
+    loads such as Q: it does not see the hand-written waits)."""
+    for name, body in _functions(asm).items():
+        for n, since in _prefetch_waits(body):
+            assert n >= since, (name, n, since)
+
+
+def test_short_ring_entries(asm):
+    """The ring entries' prologue issues K(0) and V(0) into LDS and Q into
+    registers (two, two and four loads per wave) before the first barrier,
+    and their loop has compiler waits of the kind checked above (for Q) that
+    leave the prefetch in flight.  32 KiB of LDS and <= 128 VGPRs keep four
+    blocks per compute unit."""
     occ, lds = _occupancy(asm), _lds_bytes(asm)
     rings = {n: b for n, b in _functions(asm).items() if "_short_ring_msk" in n}
     assert len(rings) == 4
@@ -144,16 +169,4 @@ def test_short_ring_prefetch_is_not_waited_on(asm):
         first = next(i for i, x in enumerate(ins) if x.startswith("s_barrier"))
         loads = [x for x in ins[:first] if x.startswith("buffer_load_dwordx4")]
         assert sorted("L" if x.endswith(" lds") else "R" for x in loads) == ["L"] * 4 + ["R"] * 4, (name, loads)
-        since_barrier, checked = None, 0
-        for i, x in enumerate(ins):
-            if x.startswith("s_barrier"):
-                since_barrier = 0
-            elif x.startswith("buffer_load_dwordx4") and since_barrier is not None:
-                since_barrier += 1
-            elif x.startswith("s_waitcnt") and "vmcnt" in x and since_barrier is not None:
-                nxt = next((y for y in ins[i + 1:] if y.startswith(("s_barrier", "ds_read"))), "s_barrier")
-                if nxt.startswith("ds_read"):
-                    n = int(re.search(r"vmcnt\((\d+)\)", x).group(1))
-                    assert n >= since_barrier, (name, i, x, since_barrier)
-                    checked += 1
-        assert checked >= 1, name
+        assert any(since > 0 for _, since in _prefetch_waits(body)), name
