@@ -263,9 +263,6 @@ def profile_forms(args):
 
 
 CLI = os.path.join(ROOT, "fmha_native_amd", "bench_fmha_fwd")
-SHORT_ROWS = 262144  # B * S * H for every short shape
-
-
 def _cli_avg(stdout, key):
     for l in stdout.splitlines():
         if l.startswith(key):
@@ -275,15 +272,16 @@ def _cli_avg(stdout, key):
 
 def profile_short(args):
     """Short sequences through the bench CLI: kernel trace per shape and form."""
-    shapes = [(m, 16384 // sq, sq) for m in (0, 1) for sq in (64, 128, 256, 512)]
+    shapes = [(m, 16384 // sq, sq) for m in (0, 1) for sq in (64, 128, 192, 256, 512)]
     md = ["# Short sequences: achieved HBM bandwidth (MI355X, one GPU)", "",
           "Every figure from one run of `python -m fmha_native_amd.rocprof --short` on one box (repo root, "
           "`TMPDIR=/tmp`); each pass is its own process under `timeout -s KILL`:", "",
           "    rocprofv3 --kernel-trace --stats -d <out>/<tag> -o run -- fmha_native_amd/bench_fmha_fwd "
           "-b <B> -h 16 -s <S> --mask <0|1> --lse 1 --dist normal --warmup 5 --iters 100 --variant <auto|regular>",
-          "", "Every shape holds the same 262,144 query rows (B·S = 16,384, H = 16), so the algorithmic HBM traffic "
-          "is the same: Q, K, V read once and O written once, 4·B·H·S·64·2 bytes, plus the 4-byte LSE per row, "
-          "135.3 MB. GB/s = those bytes ÷ the kernel's average dispatch duration (`top_kernels`, 205 dispatches: "
+          "", "Every shape holds about 262,144 query rows (B = ⌊16,384 / S⌋, H = 16), so the algorithmic HBM "
+          "traffic is about the same: Q, K, V read once and O written once, 4·B·H·S·64·2 bytes, plus the 4-byte "
+          "LSE per row, 135.3 MB at B·S = 16,384 (S192: 133.7 MB). GB/s = those bytes ÷ the kernel's average "
+          "dispatch duration (`top_kernels`, 205 dispatches: "
           "5 warm-up, 100 timed one by one, 100 back to back); the percentage is of MI355X's 8 TB/s. `auto` is "
           "the launcher's choice.", ""]
     # device copies of the same traffic: 2 x 67.1 MB (read + write) and a 3:1 read/write mix
@@ -297,7 +295,6 @@ def profile_short(args):
            f"8 TB/s): the rate a plain stream of this size reaches.", "", f"    {ccmd}", "",
            "| shape | form | kernel | avg µs | GB/s | of 8 TB/s | of the copy rate | TFLOP/s |",
            "|---|---|---|---|---|---|---|---|"]
-    io = 4 * SHORT_ROWS * 64 * 2 + 4 * SHORT_ROWS
     copy_gbs = nbytes / (cp["avg_us"] * 1e-6) / 1e9
     res = {}
     for m, b, sq in shapes:
@@ -313,7 +310,8 @@ def profile_short(args):
             if not dbs or "Avg:" not in r.stdout:
                 raise RuntimeError(f"{tag} failed (rc={r.returncode}): {r.stderr[-500:]}")
             k = [k for k in _kernel_stats(dbs[0]) if k["name"].startswith("fmha_fwd")][0]
-            gbs = io / (k["avg_us"] * 1e-6) / 1e9
+            rows = b * 16 * sq
+            gbs = (4 * rows * 64 * 2 + 4 * rows) / (k["avg_us"] * 1e-6) / 1e9
             flops = 4.0 * b * 16 * sq * sq * 64 * (0.5 if m else 1.0)
             res[(m, sq, form)] = k["avg_us"]
             md.append(f"| {'causal' if m else 'dense'} B{b} H16 S{sq} | {form} | `{k['name']}` | {k['avg_us']:.2f} | "
