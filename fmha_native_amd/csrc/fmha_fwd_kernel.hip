@@ -76,6 +76,10 @@ constexpr float kGrowSum = 65536.0f;               // tile-sum bound of the spec
 constexpr float kMaxSeed = -3.402823466e38f;       // -FLT_MAX
 constexpr uint32_t kBufferWord3 = 0x00020000u;     // raw dword buffer, gfx9 family
 constexpr int kPartFloatsPerWave = 34 * 64;        // balanced form: one wave's partial result (O^T, m, l)
+// Cache policy of the O stores: non-temporal (NT).  No block reads O back, and
+// O kept out of the caches leaves them to K/V (dense B4 H16 S2048 and causal
+// B1 H16 S8192 +1 %, short form dense B128 H16 S128 +2.5 %).
+constexpr int kStoreStream = 2;
 
 // sched_group_barrier instruction classes
 constexpr int kSchedVALU = 0x002;
@@ -698,7 +702,7 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
             const i32x4 raw = *(const lds_i32x4*)(tb + r * kRowBytes + (pc << 4));
             const i32x4 v = (r & 1) ? i32x4{raw[2], raw[3], raw[0], raw[1]} : raw;  // odd rows: halves back in order
             const int c = pc ^ ((r >> 1) & 7);
-            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * p.stride_o * 2 + c * 16, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * p.stride_o * 2 + c * 16, 0, kStoreStream);
         }
     }
     if (p.lse != nullptr && hi == 0 && my_row < sq) {
@@ -1256,19 +1260,17 @@ __device__ __forceinline__ void fwd_persistent(const Ring& ring, lds_char* qbuf)
 
 // ===========================================================================
 // Short form (this build's own; no counterpart in the reference): the
-// regular grid for launches whose keys fit two 64-key tiles (seqlen_k <= 128
-// per sequence).  A block loads all of its K and V rows into LDS at once (no
-// ring: 32 KiB) and its Q rows into registers, computes the scores of both
-// tiles, the exact softmax over them (no running max) and O, and stages O
-// through the K rows' LDS.  Such blocks are bound by memory latency, not by
-// the MFMA rate: at <= 128 VGPRs and 32 KiB of LDS four of them share a
-// compute unit (the regular form fits two), so one block's loads overlap the
-// others' work.
+// regular grid at four blocks per compute unit.  Its exact path takes
+// launches whose keys fit two 64-key tiles (seqlen_k <= 128 per sequence): a
+// block loads all of its K and V rows into LDS at once (no ring: 32 KiB) and
+// its Q rows into registers, computes the scores of both tiles, the exact
+// softmax over them (no running max) and O, and stages O through the K rows'
+// LDS.  Such blocks are bound by memory latency, not by the MFMA rate: at
+// <= 128 VGPRs and 32 KiB of LDS four of them share a compute unit (the
+// regular form fits two), so one block's loads overlap the others' work.
+// Its ring path (below) streams longer key ranges.
 // ===========================================================================
 constexpr int kShortTiles = 2;
-// Cache policy of the short form's O stores: non-temporal (NT), the rows are
-// not read again by this launch (2.5 % faster on dense B128 H16 S128).
-constexpr int kStoreStream = 2;
 
 // The ring path of the short form (longer key ranges, up to 512 keys by the
 // launcher's rule): K and V tiles in two-stage rings (32 KiB of LDS, each
