@@ -1272,8 +1272,8 @@ __device__ __forceinline__ void fwd_persistent(const Ring& ring, lds_char* qbuf)
 // ===========================================================================
 constexpr int kShortTiles = 2;
 
-// The ring path of the short form (longer key ranges, up to 512 keys by the
-// launcher's rule): K and V tiles in two-stage rings (32 KiB of LDS, each
+// The ring path of the short form (longer key ranges: the launcher picks it
+// up to 192 keys, causal 384): K and V tiles in two-stage rings (32 KiB of LDS, each
 // stage its own __shared__ array, as the regular form's rings), prefetched
 // one tile ahead; one 64-key tile per iteration whose two 32-key halves each
 // take GEMM0, an online softmax with the exact running row max and their
@@ -1826,7 +1826,7 @@ __global__ __launch_bounds__(FMHA_KBLOCK) void fmha_fwd_d64_bf16_balanced_merge(
 // ---- short entries (this build's own; no counterpart in the reference):
 // the regular grid, <= 128 VGPRs, four blocks per
 // compute unit, 32 KiB of LDS.  The exact entries take seqlen_k <= 128 (per
-// sequence), the ring entries any key count (the launcher's rule: up to 512).
+// sequence), the ring entries any key count (the launcher picks them up to 192 keys, causal 384).
 // Causal entries run the heaviest M-tiles first, as the regular ones. ----
 #define FMHA_SHORT_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
 // every K and V stage its own array
