@@ -1824,10 +1824,11 @@ __global__ __launch_bounds__(FMHA_KBLOCK) void fmha_fwd_d64_bf16_balanced_merge(
 }
 
 // ---- short entries (this build's own; no counterpart in the reference):
-// the regular grid, <= 128 VGPRs, four blocks per
-// compute unit, 32 KiB of LDS.  The exact entries take seqlen_k <= 128 (per
-// sequence), the ring entries any key count (the launcher picks them up to 192 keys, causal 384).
-// Causal entries run the heaviest M-tiles first, as the regular ones. ----
+// the regular grid, <= 128 VGPRs and 32 KiB of LDS, four blocks per compute
+// unit.  The exact entries take seqlen_k <= 128 (per sequence), the ring
+// entries any key count (the launcher picks them up to 192 keys, causal
+// 384).  Causal entries run the heaviest M-tiles first, as the regular
+// ones. ----
 #define FMHA_SHORT_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
 // every K and V stage its own array
 #define FMHA_SHORT_LDS                                                                                     \
