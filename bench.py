@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 D64 BF16 FMHA forward (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--cpu-all]
 
 Metric: forward TFLOP/s (repo FLOP convention 4*B*H*Sq*Sk*D, x0.5 when
 causal; reference src/bench_fmha_fwd.cpp:225-226) and its fraction of the
@@ -25,7 +25,10 @@ The CPU baseline is the reference's own CPU path, cpu_ref_verify, compiled
 from its sources into oracle/_ref/ref_verify and timed over the whole
 workload of both metric configurations on this host ("kind": "reference");
 where that harness was not built, the faithful C restatement (oracle/) on a
-bounded row sample ("kind": "port").  Only this leg touches oracle/.
+bounded row sample ("kind": "port").  ``--cpu-all`` adds cfg1 and cfg4 (the
+reference, whole workloads) and cfg5 (the port on a row sample: the whole
+workload takes its loop minutes on one thread).  Only this leg touches
+oracle/.
 """
 import argparse
 import json
@@ -228,11 +231,13 @@ def cpu_baseline_reference(prob, heads=None):
     None if not built."""
     import subprocess
 
-    if not os.path.exists(REF_VERIFY) or prob.varlen:
+    if not os.path.exists(REF_VERIFY):
         return None
     nh = heads or prob.nhead_q
     cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(nh), "-s", str(prob.seqlen_q), "--seed", "42",
            "--mask", str(int(prob.causal)), "--lse", str(int(prob.lse))]
+    if prob.varlen:
+        cmd += ["--varlen-seqs", ",".join(str(x) for x in prob.varlen_seqs)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         return None
@@ -249,11 +254,13 @@ def cpu_baseline_reference(prob, heads=None):
         assert -(-(prob.batch * nh) // 16) == chunks == 1, "a head sample must keep the loop's parallelism"
     t = t_run * prob.nhead_q / nh
     lse = f", LSE |d| max {res[0]['lse_max_abs']:.2e}" if prob.lse else ""
-    shape = f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''}"
+    seqs = f"varlen {'/'.join(str(x) for x in prob.varlen_seqs)} H{prob.nhead_q}" if prob.varlen else \
+        f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}"
+    shape = f"{seqs}{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''}"
     what = (f"over {nh} of the {prob.nhead_q} heads of the {shape} workload ({t_run:.2f} s, scaled x{prob.nhead_q}/{nh}"
             f" to {t:.2f} s: one thread computes every head either way, the B*H units all fitting one chunk of 16)"
             if heads else f"over the full {shape} workload, {t:.2f} s")
-    return {
+    out = {
         "value": prob.flops() / t / 1e12,
         "unit": "TFLOP/s",
         "cores": thr,
@@ -270,14 +277,19 @@ def cpu_baseline_reference(prob, heads=None):
                   f"{' (x0.5; the loop computes every masked score too)' if prob.causal else ''}; its check of "
                   f"this kernel's output: pass={res[0]['pass']}{lse}",
     }
+    if prob.varlen:
+        out["value_exact_flops"] = prob.exact_flops() / t / 1e12
+    return out
 
 
-def cpu_baseline(prob, host, budget_s=10.0):
-    """Reference-faithful oracle on rows [0, R) of every (batch, head)."""
+def cpu_baseline(prob, host, budget_s=10.0, nthreads=None):
+    """Reference-faithful oracle on rows [0, R) of every (batch, head)
+    (``nthreads``: default min(host threads, B*H))."""
     import oracle
 
     nproc, omp, threads = _host_threads()
-    nthreads = max(1, min(threads, prob.batch * prob.nhead_q))  # reference parallelises over (b, h)
+    if nthreads is None:
+        nthreads = max(1, min(threads, prob.batch * prob.nhead_q))  # reference parallelises over (b, h)
     q, k, v = host
 
     def run(rows):
@@ -305,6 +317,35 @@ def cpu_baseline(prob, host, budget_s=10.0):
                   f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}{' causal' if prob.causal else ''} (full keys), "
                   f"{t:.1f} s on {nthreads} threads; extrapolated to the whole workload at that rate",
     }
+
+
+def cpu_baseline_others():
+    """The CPU baseline on the other benchmark configurations (``--cpu-all``):
+    cfg1 and cfg4 by the reference's own cpu_ref_verify over the whole
+    workload (cfg4: eight sequences x 16 heads, 128 (sequence, head) units in
+    8 chunks of 16, so 8 threads have work); cfg5 (B1 H2 S40000, both units in
+    one chunk: one thread, about 20 minutes in full) by the C port on a row
+    sample, on one thread as the reference's loop would run it."""
+    from fmha_native_amd.problem import baseline_problems
+
+    keys = ("value", "value_exact_flops", "unit", "cores", "kind", "seconds", "effective_parallelism", "sample")
+    out = {}
+    probs = baseline_problems()
+    for name in ("cfg1", "cfg4"):
+        print(f"bench.py: CPU baseline {name}", file=sys.stderr, flush=True)
+        c = cpu_baseline_reference(probs[name][0])
+        if c is not None:
+            out[name] = {k: c[k] for k in keys if k in c}
+    import fmha_native_amd as fmha
+
+    print("bench.py: CPU baseline cfg5", file=sys.stderr, flush=True)
+    prob5, mult5 = probs["cfg5"]
+    nq, nk, _ = prob5.sizes()
+    host = (fmha.fill_normal(42, nq, mult5), fmha.fill_normal(43, nk, mult5), fmha.fill_normal(44, nk, mult5))
+    c5 = cpu_baseline(prob5, host, budget_s=20.0, nthreads=1)
+    c5["effective_parallelism"] = 1
+    out["cfg5"] = {k: c5[k] for k in keys if k in c5}
+    return out
 
 
 PROFILE_JSON = os.path.join(ROOT, "profiles", "roofline_fmha_fwd_d64_bf16_cfg2_cfg3.json")
@@ -361,6 +402,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-all", action="store_true",
+                    help="also time the CPU baseline on cfg1, cfg4 and cfg5 (about a minute more of host time)")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
     ap.add_argument("--only", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
                     help="time one workload only (profiling runs)")
@@ -431,6 +474,8 @@ def main():
         c3 = cpu_baseline_reference(cfg3, heads=4) or cpu_baseline(cfg3, r3["host"])
         cpu["cfg3"] = {k: c3[k] for k in ("value", "unit", "cores", "kind", "seconds", "effective_parallelism",
                                           "sample") if k in c3}
+        if args.cpu_all:
+            cpu.update(cpu_baseline_others())
 
     achieved = r2["tflops"]
     line = {
