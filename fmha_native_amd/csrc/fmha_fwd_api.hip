@@ -140,12 +140,10 @@ bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
-// Keys the short form's exact path holds at once (two 64-key tiles); longer
-// key ranges take its ring path.
-constexpr int kShortKeys = 2 * FMHA_KN0;
-// Keys up to which the automatic choice takes the ring path: on every grid of
-// two blocks' worth of rows per compute unit, and causal on grids of eight.
-constexpr int kShortRingKeys = 3 * FMHA_KN0, kShortRingKeysCausal = 6 * FMHA_KN0;
+// Keys up to which the automatic choice takes the short form: on every grid
+// of two blocks' worth of query rows per compute unit, and causal on grids of
+// eight.
+constexpr int kShortKeys = 3 * FMHA_KN0, kShortKeysCausal = 6 * FMHA_KN0;
 
 // blocks of the regular grid and of the pair grid
 int64_t grid_blocks(const FmhaFwdParams* p, int batch) {
@@ -155,27 +153,28 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
     return (int64_t)p->nhead_q * (((p->seqlen_q + kM0 - 1) / kM0 + 1) / 2) * batch;
 }
 
-// The automatic form of a dense launch: the short form when its keys fit
-// three tiles (seqlen_k is exact there; two tiles: the exact path, three:
-// the ring path) and the launch has at least two blocks' worth of query rows
-// per compute unit, or, causal, up to 384 keys with at least eight; else the
-// grid-shape rule above.
-// Kernel trace, H16, S64 and S128, B1-B128 (dense and causal): the exact path
-// is 9-30 % faster from 65,536 rows up (B32 S128, B64 S64) and up to 13 %
-// slower on smaller grids, where one block's latency sets the launch time
-// (B32 S64, 32,768 rows in 512 half-filled blocks: -3.5 %).  Back to back,
-// H16, 65,536-262,144 rows, against the regular form: the ring path is 8-14 %
-// faster dense at 160-192 keys, 3 % at 224, -6 to +1 % at 256-320, 2-8 %
-// slower at 384; causal 12-21 % faster at 160-192 keys at every size, 7-11 %
-// at 224-384 keys from 262,144 rows and -14 to +2 % below.  Past a few key
-// tiles the regular form's software pipeline (GEMM0 of the next tile beside
-// the softmax of this one) catches up with the ring path's four blocks per
-// compute unit; causal grids keep the ring path longer (their light M-tiles
-// are short).
-int pick_dense(const FmhaFwdParams* p, int batch, int causal, int64_t cus) {
+// The automatic form: the short form when its keys fit three tiles and the
+// launch has at least two blocks' worth of query rows per compute unit, or,
+// causal, up to 384 keys with at least eight; else the grid-shape rule above.
+// For varlen launches seqlen_k and seqlen_q are the caller's bounds (the rows
+// counted here are an upper bound); the short form reads each sequence's own
+// lengths like the other forms, so the bounds steer the choice only.
+// Kernel trace, H16, ~262,144 query rows, against the regular form: the
+// short form is 12-28 % faster at 64-128 keys (dense S128 23.2 against 26.4
+// us, causal S64 25.5 against 35.5 us); back to back, H16, 65,536-262,144 rows: 8-14 % faster dense at
+// 160-192 keys, 3 % at 224, -6 to +1 % at 256-320, 2-8 % slower at 384;
+// causal 12-21 % faster at 160-192 keys at every size, 7-11 % at 224-384
+// keys from 262,144 rows and -14 to +2 % below.  On smaller grids one
+// block's latency sets the launch time and the regular form wins (B1 H2
+// S128: 4.6 against 5.6 us).  Varlen batches of 256-2048 sequences of 16-192
+// tokens, H16: 13-33 % faster.  Past a few key tiles the regular form's
+// software pipeline (GEMM0 of the next tile beside the softmax of this one)
+// catches up with the short form's four blocks per compute unit; causal
+// grids keep the short form longer (their light M-tiles are short).
+int pick_form(const FmhaFwdParams* p, int batch, int causal, int64_t cus) {
     const int64_t rows = (int64_t)batch * p->nhead_q * p->seqlen_q;
-    if (p->seqlen_k <= kShortRingKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
-    if (causal && p->seqlen_k <= kShortRingKeysCausal && rows >= 8 * cus * kM0) return FMHA_VARIANT_SHORT;
+    if (p->seqlen_k <= kShortKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
+    if (causal && p->seqlen_k <= kShortKeysCausal && rows >= 8 * cus * kM0) return FMHA_VARIANT_SHORT;
     return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
 }
 
@@ -367,8 +366,7 @@ extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, in
 extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch, int causal, int compute_units) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
     const int64_t cus = compute_units > 0 ? compute_units : device_cus();
-    if (p->seqstart_q != nullptr) return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
-    return pick_dense(p, batch, causal, cus);
+    return pick_form(p, batch, causal, cus);
 }
 
 extern "C" int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* p, int batch, int causal) {
@@ -411,18 +409,12 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
         return hipGetLastError();
     }
     if (variant == FMHA_VARIANT_AUTO)
-        variant = varlen ? pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, device_cus())
-                         : pick_dense(p, batch, causal, device_cus());
+        variant = pick_form(p, batch, causal, device_cus());
     if (variant == FMHA_VARIANT_SHORT) {
-        // the exact path when seqlen_k (every sequence's bound) fits two tiles
         using Entry = void (*)(FmhaFwdParams);
-        static const Entry entries[2][2][2] = {
-            {{fmha_fwd_d64_bf16_short_msk0, fmha_fwd_d64_bf16_short_msk0_varlen},
-             {fmha_fwd_d64_bf16_short_msk1, fmha_fwd_d64_bf16_short_msk1_varlen}},
-            {{fmha_fwd_d64_bf16_short_ring_msk0, fmha_fwd_d64_bf16_short_ring_msk0_varlen},
-             {fmha_fwd_d64_bf16_short_ring_msk1, fmha_fwd_d64_bf16_short_ring_msk1_varlen}}};
-        const Entry e = entries[p->seqlen_k > kShortKeys ? 1 : 0][causal ? 1 : 0][varlen ? 1 : 0];
-        hipLaunchKernelGGL(e, grid, dim3(kBlockSize), 0, stream, *p);
+        static const Entry entries[2][2] = {{fmha_fwd_d64_bf16_short_msk0, fmha_fwd_d64_bf16_short_msk0_varlen},
+                                            {fmha_fwd_d64_bf16_short_msk1, fmha_fwd_d64_bf16_short_msk1_varlen}};
+        hipLaunchKernelGGL(entries[causal ? 1 : 0][varlen ? 1 : 0], grid, dim3(kBlockSize), 0, stream, *p);
         return hipGetLastError();
     }
     if (tile_major) {  // causal, dense, batch > 1

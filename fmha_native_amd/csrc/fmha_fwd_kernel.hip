@@ -1260,32 +1260,22 @@ __device__ __forceinline__ void fwd_persistent(const Ring& ring, lds_char* qbuf)
 
 // ===========================================================================
 // Short form (this build's own; no counterpart in the reference): the
-// regular grid at four blocks per compute unit.  Its exact path takes
-// launches whose keys fit two 64-key tiles (seqlen_k <= 128 per sequence): a
-// block loads all of its K and V rows into LDS at once (no ring: 32 KiB) and
-// its Q rows into registers, computes the scores of both tiles, the exact
-// softmax over them (no running max) and O, and stages O through the K rows'
-// LDS.  Such blocks are bound by memory latency, not by the MFMA rate: at
-// <= 128 VGPRs and 32 KiB of LDS four of them share a compute unit (the
-// regular form fits two), so one block's loads overlap the others' work.
-// Its ring path (below) streams longer key ranges.
+// regular grid at four blocks per compute unit (<= 128 VGPRs and 32 KiB of
+// LDS; the regular form fits two), for launches whose M-tiles see few key
+// tiles.  Such blocks are bound by memory latency more than by the MFMA
+// rate, so one block's loads overlap the other three's work.  K and V tiles
+// stream through two-stage rings (each stage its own __shared__ array, as the
+// regular form's rings), prefetched one tile ahead; each 64-key tile is taken
+// as two 32-key halves (GEMM0, an online softmax with the exact running row
+// max, that half's GEMM1), so a wave holds 16 scores at a time.  Any number
+// of key tiles works; the launcher picks the form up to 192 keys (causal 384).
 // ===========================================================================
-constexpr int kShortTiles = 2;
-
-// The ring path of the short form (longer key ranges: the launcher picks it
-// up to 192 keys, causal 384): K and V tiles in two-stage rings (32 KiB of LDS, each
-// stage its own __shared__ array, as the regular form's rings), prefetched
-// one tile ahead; one 64-key tile per iteration whose two 32-key halves each
-// take GEMM0, an online softmax with the exact running row max and their
-// share of GEMM1 (half a tile of scores at a time keeps the wave within 128
-// VGPRs).
-// The exact path holds its two tiles in the same four arrays.
 struct ShortLds {
     lds_char* k[2];
     lds_char* v[2];
 };
 
-template <bool kCausal, bool kVarlen, bool kRingPath>
+template <bool kCausal, bool kVarlen>
 __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, int mt, const ShortLds& lds) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1330,12 +1320,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
         const int e = last + shift + 1;
         kv_end = e < 0 ? 0 : (e > sk ? sk : e);
     }
-    const int ntiles = (kv_end + kTileN - 1) / kTileN;  // exact path: <= 2 (the launcher's rule)
-    // A varlen sequence with more keys than the exact path holds breaks the
-    // caller's promise (seqlen_k bounds every sequence): its rows get NaN in O
-    // and LSE instead of a softmax over its first 128 keys.  The ring path
-    // takes any number of keys.
-    const bool too_long = !kRingPath && kVarlen && ntiles > kShortTiles;
+    const int ntiles = (kv_end + kTileN - 1) / kTileN;
     const int wrow0 = row0 + wave * kRowsPerWave;
     const int my_row = wrow0 + l32;
     const int ld_row = 2 * wave * 8 + (lane >> 3);
@@ -1346,7 +1331,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
     const float scale = p.scale;
     const float scale_v = in_vgpr(scale);
     const int g = lane >> 4, i16 = lane & 15, e4 = i16 >> 2, c4 = i16 & 3;
-    float m_ref, l_part = 0.0f;
+    float m_ref = kMaxSeed, l_part = 0.0f;  // the running max starts below every score
     f32x16 oacc[2];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
@@ -1408,162 +1393,98 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
                 oacc[db] = mfma(lds_read_vt(vt + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[k], oacc[db]);
     };
 
-    if constexpr (!kRingPath) {
-        // K rows into LDS, Q rows into registers, then V rows into LDS (tile t
-        // at t * 8 KiB).  The scores wait only for K and Q (vmcnt counts the four
-        // V loads still in flight), GEMM1 for V.
+    // prologue: K(0), Q, V(0).  Iteration t (stage J = t % 2) waits for
+    // K(t), V(t) (and Q), then prefetches tile t+1 into the other stage,
+    // which tile t-1 used (every wave is past it after the barrier), and
+    // computes tile t while those loads fly.
+    issue_k(0, lds.k[0]);
+    load_q();
+    issue_v(0, lds.v[0]);
+    // scores of one 32-key half: GEMM0, then the mask (keys >= sk, causal
+    // keys > row + shift) where the half reaches past it
+    auto scores = [&](const lds_char* kt, int t, int kb, f32x16& s) {
+        s = f32x16{};
+        gemm0_half(kt, kb, s);
+        const int d = lim - (t * kTileN + 32 * kb + 4 * hi);
+        if (__builtin_amdgcn_ballot_w64(d < 31)) {
 #pragma unroll
-        for (int t = 0; t < kShortTiles; ++t) issue_k(t, lds.k[t]);
-        load_q();
-#pragma unroll
-        for (int t = 0; t < kShortTiles; ++t) issue_v(t, lds.v[t]);
-        vmcnt_wait<2 * kShortTiles>();
-        ring_barrier();
-
-        f32x16 sacc[kShortTiles][2];
-#pragma unroll
-        for (int t = 0; t < kShortTiles; ++t)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                f32x16 acc = {};
-                if (t < ntiles) gemm0_half(lds.k[t], kb, acc);
-                sacc[t][kb] = acc;
+            for (int r = 0; r < 16; ++r) {
+                const int c = 8 * (r >> 2) + (r & 3);
+                s[r] = c <= d ? s[r] : ninf;
             }
-        // mask (keys >= sk, causal keys > row + shift, and the tiles past ntiles),
-        // then the exact row max over both tiles
+        }
+    };
+    // exact max of the half's rows, scaled (-inf for a row with no key)
+    auto half_max = [&](const f32x16& s) {
         float mx = ninf;
 #pragma unroll
-        for (int t = 0; t < kShortTiles; ++t) {
-            const int d = lim - (t * kTileN + 4 * hi);
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
-                    sacc[t][kb][r] = (c <= d && t < ntiles) ? sacc[t][kb][r] : ninf;
-                    mx = fmaxf(mx, sacc[t][kb][r]);
-                }
-        }
-        m_ref = fmaxf(kMaxSeed, wave_max_halves(mx) * scale);  // -FLT_MAX for a row with no key
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        return wave_max_halves(mx) * scale;
+    };
+    // P = exp2(s*scale - m_ref), bf16-packed, and this lane's sum of P
+    // (fp32, before the rounding)
+    auto exp_half = [&](const f32x16& s, bf16x8* pp) {
         const float neg_ms = -m_ref;
-        vmcnt_wait<0>();  // V
+        float ls[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            bf16x8 pk;
+            float acc;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * k + e], scale_v, neg_ms));
+                acc = e == 0 ? pv : acc + pv;
+                pk[e] = (__bf16)pv;
+            }
+            ls[k] = acc;
+            pp[k] = pk;
+        }
+        return ls[0] + ls[1];
+    };
+    // online softmax with the exact running row max of each half; O^T and
+    // l move to a new max only where it grew (always at a row's first
+    // visible keys, rarely after).  The regular form's speculative frame
+    // would save the max but needs the scores and P live together on its
+    // re-framing path, past 128 VGPRs.
+    auto iteration = [&](int t, auto stage_c) {
+        constexpr int J = decltype(stage_c)::value;
+        vmcnt_wait<0>();
         ring_barrier();
+        issue_k(t + 1, lds.k[J ^ 1]);
+        issue_v(t + 1, lds.v[J ^ 1]);
+        lds_char* const kt = lds.k[J];
+        lds_char* const vt = lds.v[J];
 #pragma unroll
-        for (int t = 0; t < kShortTiles; ++t) {
-            if (t < ntiles) {
-                bf16x8 pp[4];
+        for (int kb = 0; kb < 2; ++kb) {
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 sacc;
+            scores(kt, t, kb, sacc);
+            const float m_new = fmaxf(m_ref, half_max(sacc));
+            if (__builtin_amdgcn_ballot_w64(m_new > m_ref)) {
+                const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int db = 0; db < 2; ++db)
 #pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        bf16x8 pk;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][kb][8 * k + e], scale_v, neg_ms));
-                            l_part += pv;
-                            pk[e] = (__bf16)pv;
-                        }
-                        pp[2 * kb + k] = pk;
-                    }
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) gemm1_half(lds.v[t], kb, pp + 2 * kb);
+                    for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+                l_part *= alpha;
+                m_ref = m_new;
             }
+            bf16x8 pp[2];
+            l_part += exp_half(sacc, pp);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm1_half(vt, kb, pp);
         }
-    } else {
-        // prologue: K(0), Q, V(0).  Iteration t (stage J = t % 2) waits for
-        // K(t), V(t) (and Q), then prefetches tile t+1 into the other stage,
-        // which tile t-1 used (every wave is past it after the barrier), and
-        // computes tile t while those loads fly.
-        issue_k(0, lds.k[0]);
-        load_q();
-        issue_v(0, lds.v[0]);
-        m_ref = kMaxSeed;
-        // scores of one 32-key half: GEMM0, then the mask (keys >= sk, causal
-        // keys > row + shift) where the half reaches past it
-        auto scores = [&](const lds_char* kt, int t, int kb, f32x16& s) {
-            s = f32x16{};
-            gemm0_half(kt, kb, s);
-            const int d = lim - (t * kTileN + 32 * kb + 4 * hi);
-            if (__builtin_amdgcn_ballot_w64(d < 31)) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int c = 8 * (r >> 2) + (r & 3);
-                    s[r] = c <= d ? s[r] : ninf;
-                }
-            }
-        };
-        // exact max of the half's rows, scaled (-inf for a row with no key)
-        auto half_max = [&](const f32x16& s) {
-            float mx = ninf;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
-            return wave_max_halves(mx) * scale;
-        };
-        // P = exp2(s*scale - m_ref), bf16-packed, and this lane's sum of P
-        // (fp32, before the rounding)
-        auto exp_half = [&](const f32x16& s, bf16x8* pp) {
-            const float neg_ms = -m_ref;
-            float ls[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                bf16x8 pk;
-                float acc;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * k + e], scale_v, neg_ms));
-                    acc = e == 0 ? pv : acc + pv;
-                    pk[e] = (__bf16)pv;
-                }
-                ls[k] = acc;
-                pp[k] = pk;
-            }
-            return ls[0] + ls[1];
-        };
-        // online softmax with the exact running row max of each half; O^T and
-        // l move to a new max only where it grew (always at a row's first
-        // visible keys, rarely after).  The regular form's speculative frame
-        // would save the max but needs the scores and P live together on its
-        // re-framing path, past 128 VGPRs.
-        auto iteration = [&](int t, auto stage_c) {
-            constexpr int J = decltype(stage_c)::value;
-            vmcnt_wait<0>();
-            ring_barrier();
-            issue_k(t + 1, lds.k[J ^ 1]);
-            issue_v(t + 1, lds.v[J ^ 1]);
-            lds_char* const kt = lds.k[J];
-            lds_char* const vt = lds.v[J];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                __builtin_amdgcn_sched_barrier(0);
-                f32x16 sacc;
-                scores(kt, t, kb, sacc);
-                const float m_new = fmaxf(m_ref, half_max(sacc));
-                if (__builtin_amdgcn_ballot_w64(m_new > m_ref)) {
-                    const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
-#pragma unroll
-                    for (int db = 0; db < 2; ++db)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-                    l_part *= alpha;
-                    m_ref = m_new;
-                }
-                bf16x8 pp[2];
-                l_part += exp_half(sacc, pp);
-                __builtin_amdgcn_sched_barrier(0);
-                gemm1_half(vt, kb, pp);
-            }
-        };
-        for (int t = 0; t < ntiles; t += 2) {
-            iteration(t, std::integral_constant<int, 0>{});
-            if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{});
-        }
-        vmcnt_wait<0>();  // the last iteration's (empty) refills
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+        iteration(t, std::integral_constant<int, 0>{});
+        if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{});
     }
+    vmcnt_wait<0>();  // the last iteration's (empty) refills
 
     // epilogue: O = O^T / l through this wave's rows of the K tile area (every
     // wave's K reads are done after the barrier), LSE
     const float l_tot = wave_sum_halves(l_part);
-    const float inv = too_long ? __builtin_nanf("") : l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     ring_barrier();
     lds_char* const tb = (wave < 2 ? lds.k[0] : lds.k[1]) + (wave & 1) * (kRowsPerWave * kRowBytes);
 #pragma unroll
@@ -1597,7 +1518,7 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
             lse_base = p.lse + (int64_t)h * (p.nhead_stride_q / p.stride_q) + off_q;
         else
             lse_base = p.lse + (int64_t)b * p.nhead_q * p.seqlen_q + (int64_t)h * p.seqlen_q;
-        lse_base[my_row] = too_long ? __builtin_nanf("") : (__builtin_log2f(l_tot) + m_ref) * 0.69314718055994530942f;
+        lse_base[my_row] = (__builtin_log2f(l_tot) + m_ref) * 0.69314718055994530942f;
     }
 }
 
@@ -1824,29 +1745,21 @@ __global__ __launch_bounds__(FMHA_KBLOCK) void fmha_fwd_d64_bf16_balanced_merge(
 }
 
 // ---- short entries (this build's own; no counterpart in the reference):
-// the regular grid, <= 128 VGPRs and 32 KiB of LDS, four blocks per compute
-// unit.  The exact entries take seqlen_k <= 128 (per sequence), the ring
-// entries any key count (the launcher picks them up to 192 keys, causal
-// 384).  Causal entries run the heaviest M-tiles first, as the regular
-// ones. ----
+// the regular grid and block, <= 128 VGPRs and 32 KiB of LDS (four blocks
+// per compute unit), any key count.  Causal entries run the heaviest M-tiles
+// first, as the regular ones. ----
 #define FMHA_SHORT_ATTRS __global__ __launch_bounds__(FMHA_KBLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
 // every K and V stage its own array
 #define FMHA_SHORT_LDS                                                                                     \
     __shared__ __attribute__((aligned(1024))) char k0[kTileBytes], k1[kTileBytes], v0[kTileBytes], v1[kTileBytes]; \
     const ShortLds lds{{(lds_char*)k0, (lds_char*)k1}, {(lds_char*)v0, (lds_char*)v1}};
-#define FMHA_SHORT_ENTRY(name, causal, varlen, ring)                                                       \
+#define FMHA_SHORT_ENTRY(name, causal, varlen)                                                             \
     FMHA_SHORT_ATTRS void name(FmhaFwdParams params) {                                                     \
         FMHA_SHORT_LDS                                                                                      \
-        fwd_short<causal, varlen, FMHA_SHORT_IS_##ring>(params, blockIdx.z, blockIdx.x,                      \
-                                                        causal ? gridDim.y - 1 - blockIdx.y : blockIdx.y, lds); \
+        fwd_short<causal, varlen>(params, blockIdx.z, blockIdx.x, causal ? gridDim.y - 1 - blockIdx.y : blockIdx.y, \
+                                  lds);                                                                     \
     }
-#define FMHA_SHORT_IS_EXACT false
-#define FMHA_SHORT_IS_RING true
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0, false, false, EXACT)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1, true, false, EXACT)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0_varlen, false, true, EXACT)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1_varlen, true, true, EXACT)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk0, false, false, RING)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk1, true, false, RING)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk0_varlen, false, true, RING)
-FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_ring_msk1_varlen, true, true, RING)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0, false, false)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1, true, false)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk0_varlen, false, true)
+FMHA_SHORT_ENTRY(fmha_fwd_d64_bf16_short_msk1_varlen, true, true)

@@ -112,9 +112,10 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 
 /* The same launch with the kernel form chosen by the caller (this build's
  * own; no counterpart in the reference):
- *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: short for dense
+ *   FMHA_VARIANT_AUTO     what fmha_fwd_d64_bf16() picks: short for
  *                         launches with seqlen_k <= 192 and at least
- *                         2 x CUs x 128 query rows, or causal with
+ *                         2 x CUs x 128 query rows (batch x nhead_q x
+ *                         seqlen_q; varlen: the bounds), or causal with
  *                         seqlen_k <= 384 and at least 8 x CUs x 128; with
  *                         seqlen_k >= 2048,
  *                         split-KV when the regular grid has at most one
@@ -134,13 +135,9 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         into the next; its queue counters live in the
  *                         library (device memory it owns, no allocation per
  *                         call; at most 64 such launches in flight per device)
- *   FMHA_VARIANT_SHORT    the regular grid at four blocks per compute unit:
- *                         with seqlen_k <= 128 the exact entries, which load
- *                         all keys at once (varlen: seqlen_k must bound every
- *                         sequence's key length; the rows of a longer
- *                         sequence get NaN in O and LSE), else the ring
- *                         entries, which stream any number of keys through
- *                         a three-stage K and two-stage V ring
+ *   FMHA_VARIANT_SHORT    the short entries: the regular grid at four blocks
+ *                         per compute unit, K and V streamed through
+ *                         two-stage LDS rings, any number of keys
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
@@ -303,16 +300,11 @@ __global__ void fmha_fwd_d64_bf16_pair_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1_varlen(FmhaFwdParams params);
 /* Short forms (no counterpart in the reference): the regular grid and
- * block, four blocks per compute unit.  The exact entries take seqlen_k <= 128
- * (32 KiB of LDS); the ring entries any key count (40 KiB). */
+ * block, four blocks per compute unit (32 KiB of LDS), any key count. */
 __global__ void fmha_fwd_d64_bf16_short_msk0(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_short_msk1(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_short_msk0_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_short_msk1_varlen(FmhaFwdParams params);
-__global__ void fmha_fwd_d64_bf16_short_ring_msk0(FmhaFwdParams params);
-__global__ void fmha_fwd_d64_bf16_short_ring_msk1(FmhaFwdParams params);
-__global__ void fmha_fwd_d64_bf16_short_ring_msk0_varlen(FmhaFwdParams params);
-__global__ void fmha_fwd_d64_bf16_short_ring_msk1_varlen(FmhaFwdParams params);
 /* Tile-major causal dense forms (no counterpart in the reference): grid
  * (nhead_q, batch, tiles), tiles = ceil(seqlen_q/kM0) (pair form: pairs of
  * them), block kBlockSize (regular) or FMHA_SPLIT_KBLOCK; block z runs M-tile

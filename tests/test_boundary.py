@@ -30,7 +30,7 @@ KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_
                   "fmha_fwd_d64_bf16_msk1_varlen"]
 SPLIT_ENTRIES = [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("splitkv", "pair") for m in (0, 1)
                  for v in ("", "_varlen")] + [f"fmha_fwd_d64_bf16_{f}msk1_tilemajor" for f in ("", "splitkv_", "pair_")] \
-    + [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("short", "short_ring") for m in (0, 1) for v in ("", "_varlen")]
+    + [f"fmha_fwd_d64_bf16_short_msk{m}{v}" for m in (0, 1) for v in ("", "_varlen")]
 
 
 def header_c_functions():
@@ -218,11 +218,12 @@ R, S, P = fmha.VARIANT_REGULAR, fmha.VARIANT_SPLITKV, fmha.VARIANT_PAIR
 
 
 def test_short_form_rule():
-    """Dense launches whose keys fit three 64-key tiles take the short form
-    (their seqlen_k is exact) once they hold two blocks' worth of query rows
-    per compute unit (2 x CUs x 128 rows), causal ones with up to 384 keys
-    once they hold eight; smaller grids and varlen ones keep the grid-shape
-    rule (a varlen seqlen_k is only a bound the caller gives)."""
+    """Launches whose keys fit three 64-key tiles take the short form once
+    they hold two blocks' worth of query rows per compute unit (2 x CUs x 128
+    rows), causal ones with up to 384 keys once they hold eight; varlen ones
+    by their bounds (batch x nhead_q x seqlen_q rows, seqlen_k keys: the
+    short form reads each sequence's own lengths, so the bounds only steer
+    the choice); smaller grids keep the grid-shape rule."""
     # valid_params: 4 heads x 128 query rows per batch -> 512 rows
     for sk, batch, cus, dense, causal_short in (
             (1, 128, 256, True, True), (64, 128, 256, True, True), (128, 128, 256, True, True),
@@ -235,7 +236,12 @@ def test_short_form_rule():
         for causal, short in ((0, dense), (1, causal_short)):
             got = fmha.pick_variant(_mut(seqlen_k=sk, lse=None), batch, causal, cus)
             assert (got == fmha.VARIANT_SHORT) if short else (got in (R, S, P)), (sk, batch, cus, causal, got)
-    assert fmha.pick_variant(valid_params(varlen=True, lse=False), 4096, 1, 256) in (R, S, P)
+    # varlen: valid_params bounds 128 keys and 128 query rows per sequence, 4 heads
+    pv = valid_params(varlen=True, lse=False)
+    assert fmha.pick_variant(pv, 4096, 1, 256) == fmha.VARIANT_SHORT
+    assert fmha.pick_variant(pv, 127, 1, 256) in (R, S, P)
+    pv.seqlen_k = 4096
+    assert fmha.pick_variant(pv, 4096, 1, 256) in (R, S, P)
 
 
 @pytest.mark.parametrize("batch,heads,seqlen,causal,cus,form", [

@@ -6,9 +6,8 @@ s_barrier of every entry, the wave has no LDS read in flight (an
 ``s_waitcnt lgkmcnt(0)`` follows the last ds_read).  A read left in flight
 would race with the other waves' DMA refill of its stage right after the
 barrier.  Also: no entry spills to scratch, every entry keeps two waves per
-SIMD (the short form four), no compiler-inserted wait holds a tile's reads
-until the next tile's prefetch lands, and the short form's exact entries
-issue their loads in the order their first wait counts on (K, Q, V).
+SIMD (the short form four), and no compiler-inserted wait holds a tile's
+reads until the next tile's prefetch lands.
 """
 import os
 import re
@@ -53,10 +52,9 @@ def test_every_entry_compiled(asm):
         assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
     for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_merge"):
         assert any(e in n for n in names), e
-    for form in ("short_", "short_ring_"):
-        for m in (0, 1):
-            for v in ("", "_varlen"):
-                assert any(f"fmha_fwd_d64_bf16_{form}msk{m}{v}13FmhaFwdParams" in n for n in names), (form, m, v)
+    for m in (0, 1):
+        for v in ("", "_varlen"):
+            assert any(f"fmha_fwd_d64_bf16_short_msk{m}{v}13FmhaFwdParams" in n for n in names), (m, v)
 
 
 def test_no_lds_read_in_flight_at_barriers(asm):
@@ -89,28 +87,6 @@ def _occupancy(src):
     for m in re.finditer(r"^\s*\.set\s+(_Z[^.\s]+)\.has_indirect_call.*?; Occupancy: (\d+)", src, re.M | re.S):
         occ[m.group(1)] = int(m.group(2))
     return occ
-
-
-def test_short_form_issue_order_and_occupancy(asm):
-    """The short form issues its K loads into LDS, then Q into registers,
-    then V into LDS, and waits vmcnt(4) before its first barrier: that wait
-    covers K and Q only when the four V loads are the last ones issued.  It
-    keeps four waves per SIMD (four blocks per compute unit)."""
-    occ = _occupancy(asm)
-    shorts = {n: b for n, b in _functions(asm).items() if "_short_msk" in n}
-    assert len(shorts) == 4
-    for name, body in shorts.items():
-        assert occ.get(name) == 4, (name, occ.get(name))
-        seq = []
-        for line in body.splitlines():
-            ins = line.strip()
-            if ins.startswith("buffer_load_dwordx4"):
-                seq.append("L" if ins.endswith(" lds") else "R")
-            elif ins.startswith("s_barrier"):
-                break
-            elif ins.startswith("s_waitcnt") and "vmcnt" in ins:
-                seq.append(re.search(r"vmcnt\((\d+)\)", ins).group(0))
-        assert seq == ["L"] * 4 + ["R"] * 4 + ["L"] * 4 + ["vmcnt(4)"], (name, seq)
 
 
 def _lds_bytes(src):
@@ -153,14 +129,14 @@ def test_no_wait_covers_a_prefetch(asm):
             assert n >= since, (name, n, since)
 
 
-def test_short_ring_entries(asm):
-    """The ring entries' prologue issues K(0) and V(0) into LDS and Q into
+def test_short_entries(asm):
+    """The short entries' prologue issues K(0) and V(0) into LDS and Q into
     registers (two, two and four loads per wave) before the first barrier,
     and their loop has compiler waits of the kind checked above (for Q) that
     leave the prefetch in flight.  32 KiB of LDS and <= 128 VGPRs keep four
     blocks per compute unit."""
     occ, lds = _occupancy(asm), _lds_bytes(asm)
-    rings = {n: b for n, b in _functions(asm).items() if "_short_ring_msk" in n}
+    rings = {n: b for n, b in _functions(asm).items() if "_short_msk" in n}
     assert len(rings) == 4
     for name, body in rings.items():
         assert occ.get(name) == 4, (name, occ.get(name))
