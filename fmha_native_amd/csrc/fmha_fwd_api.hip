@@ -160,8 +160,8 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
 // counted here are an upper bound); the short form reads each sequence's own
 // lengths like the other forms, so the bounds steer the choice only.
 // Kernel trace, H16, ~262,144 query rows, against the regular form: the
-// short form is 12-28 % faster at 64-128 keys (dense S128 23.2 against 26.4
-// us, causal S64 25.5 against 35.5 us); back to back, H16, 65,536-262,144 rows: 8-14 % faster dense at
+// short form is 12-29 % faster at 64-128 keys (dense S128 22.7 against 25.9
+// us, causal S64 24.8 against 35.1 us); back to back, H16, 65,536-262,144 rows: 8-14 % faster dense at
 // 160-192 keys, 3 % at 224, -6 to +1 % at 256-320, 2-8 % slower at 384;
 // causal 12-21 % faster at 160-192 keys at every size, 7-11 % at 224-384
 // keys from 262,144 rows and -14 to +2 % below.  On smaller grids one
