@@ -502,6 +502,27 @@ def test_short_varlen_takes_any_key_count(causal):
     assert res["pass"], res
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_auto_takes_short_for_a_varlen_batch_of_short_sequences(causal):
+    """600 sequences of 20-190 tokens, H2: by its bounds (190 keys, 600 x 2 x
+    190 query rows) the automatic choice is the short form, and its output
+    matches the oracle."""
+    rng = np.random.default_rng(600 + int(causal))
+    seqs = tuple(int(x) for x in rng.integers(20, 191, 600))
+    p = Problem(batch=0, nhead_q=2, seqlen_q=0, causal=causal, lse=True, varlen_seqs=seqs)
+    import torch
+
+    from harness import build_params
+
+    nq, nk, nlse = p.sizes()
+    t = [torch.zeros(n, dtype=torch.int16, device="cuda:0") for n in (nq, nk, nk, nq)]
+    prm = build_params(p, *t, None, torch.from_numpy(p.seqstart()).to("cuda:0"))
+    assert fmha.pick_variant(prm, p.batch, int(causal), 256) == fmha.VARIANT_SHORT
+    print("launch: auto varlen", len(seqs), "sequences, causal", causal, flush=True)
+    res = _report(check_problem(p, dist="ref", seed=17, rule="reference", variant=fmha.VARIANT_AUTO))
+    assert res["pass"], res
+
+
 @pytest.mark.parametrize("sq,sk", [(2000, 2000), (700, 1500), (1500, 700)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_short_equals_regular_on_long_rows(causal, sq, sk):
