@@ -107,10 +107,15 @@ int device_cus() { return device_shape().cus; }
 //    blocks a CU holds in the regular form progress unevenly, so each CU's
 //    last block runs alone; a pair block has no such tail, but pays a barrier
 //    across 8 waves.  It wins when the pair blocks fill whole rounds of the
-//    CUs and the M-tiles are long: +3-4% dense at seqlen_k >= 8192, +3-5%
-//    causal at >= 32768; with a partial last round it loses 8-17%.
-//  * regular: everything else (the dense B4 H16 S2048 and causal B1 H16 S8192
-//    benchmark grids among them).
+//    CUs: dense from seqlen_k >= 2048 (+1.3-5 % at 1-4 rounds, 2048-32768
+//    keys; the dense B4 H16 S2048 benchmark grid +1.4-2.6 %); causal at
+//    exactly two rounds from 8192 keys (+3.1-4.5 %, the causal B1 H16 S8192
+//    benchmark grid +3.4-3.7 %: each CU gets one heavy and one light pair,
+//    heaviest first), or at any whole number from 32768 (+1 % at four).
+//    Causal at one round loses ~20 % (split-KV takes those grids), at three
+//    4-5 %, at four up to 4096 keys 1-4 %; dense at 1024 keys -3.5 to +2.6 %;
+//    any partial last round 8-17 %.
+//  * regular: everything else.
 int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_t cus) {
     // blocks (up to ~2^63) is only compared, never multiplied; cus < 2^31
     if (seqlen_k >= 2048) {
@@ -118,7 +123,9 @@ int pick_variant(int64_t blocks, int64_t pairs, int causal, int seqlen_k, int64_
         if (causal && (blocks <= 3 * cus / 2 || (blocks <= 2 * cus && seqlen_k >= 8192))) return FMHA_VARIANT_SPLITKV;
     }
     const bool whole_rounds = pairs >= cus && pairs % cus == 0;
-    if (whole_rounds && seqlen_k >= (causal ? 32768 : 8192)) return FMHA_VARIANT_PAIR;
+    if (!causal && whole_rounds && seqlen_k >= 2048) return FMHA_VARIANT_PAIR;
+    if (causal && ((pairs == 2 * cus && seqlen_k >= 8192) || (whole_rounds && seqlen_k >= 32768)))
+        return FMHA_VARIANT_PAIR;
     return FMHA_VARIANT_REGULAR;
 }
 

@@ -122,8 +122,9 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         block per compute unit (causal: at most 1.5, or up
  *                         to 2 with seqlen_k >= 8192); pair when its blocks
  *                         fill whole rounds of the compute units and
- *                         seqlen_k >= 8192 (causal: >= 32768); else the
- *                         regular entries
+ *                         seqlen_k >= 2048 (causal: exactly two rounds and
+ *                         seqlen_k >= 8192, or whole rounds and >= 32768);
+ *                         else the regular entries
  *   FMHA_VARIANT_REGULAR  the four reference-named entries (kBlockSize threads)
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block

@@ -256,15 +256,24 @@ def test_short_form_rule():
     (1, 13, 4096, 1, 256, R),    # 416 causal blocks, short M-tiles
     (1, 8, 8192, 1, 256, S),     # 512 causal blocks with seqlen_k >= 8192
     (1, 32, 2048, 1, 256, R),    # 512 causal blocks, short M-tiles
-    (4, 16, 2048, 0, 256, R),    # cfg2
-    (1, 16, 8192, 1, 256, R),    # cfg3: whole pair rounds but seqlen_k < 32768
+    (4, 16, 2048, 0, 256, P),    # cfg2: 512 pair blocks = 2 whole rounds
+    (1, 16, 8192, 1, 256, P),    # cfg3: 512 causal pair blocks = exactly 2 rounds
     (1, 8, 8192, 0, 256, P),     # 256 pair blocks, long M-tiles
     (1, 4, 32768, 1, 256, P),    # 512 causal pair blocks, seqlen_k >= 32768
+    (1, 8, 32768, 1, 256, P),    # 1024 causal pair blocks (4 rounds), seqlen_k >= 32768
+    (1, 32, 8192, 1, 256, R),    # 1024 causal pair blocks (4 rounds) below 32768 keys
+    (1, 24, 8192, 1, 256, R),    # 768 causal pair blocks (3 rounds)
+    (2, 16, 4096, 1, 256, R),    # 2 causal rounds but seqlen_k < 8192
+    (4, 16, 2048, 1, 256, R),    # causal S2048
+    (1, 32, 2048, 0, 256, P),    # 256 dense pair blocks (1 round) at 2048 keys
+    (8, 16, 1024, 0, 256, R),    # dense, whole rounds, but 1024 keys
+    (5, 16, 2048, 0, 256, R),    # 640 dense pair blocks: a partial last round
     (1, 2, 40000, 0, 256, R),    # 314 pair blocks: a partial last round
     (1, 2, 40000, 1, 256, R),    # cfg5
     (1, 8, 4096, 0, 304, S),     # the rule scales with the CU count
-    (4, 16, 2048, 0, 304, R),
+    (4, 16, 2048, 0, 304, R),    # 512 pair blocks: not whole rounds of 304
     (1, 19, 8192, 0, 304, P),    # 19 * 32 = 608 pair blocks = 2 rounds of 304
+    (1, 19, 8192, 1, 304, P),    # the same, causal: exactly 2 rounds
 ])
 def test_auto_form_rule(batch, heads, seqlen, causal, cus, form):
     """The launcher's documented rule (grid shape -> kernel form), host only."""
