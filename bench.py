@@ -197,7 +197,8 @@ def time_problem(prob, steps, warmup, torch, mult=1.0, variant=0):
     ref_ms = sum(times) / steps
     hip.destroy([e0, e1])
     picked = variant or fmha.pick_variant(p, batch, causal)
-    form = "balanced (two launches: items, then the merge of split M-tiles)" if need > 0 else \
+    form = ("balanced pair" if variant == fmha.VARIANT_BALANCED_PAIR else "balanced") + \
+        " (two launches: items, then the merge of split M-tiles)" if need > 0 else \
         {v: k for k, v in fmha.VARIANTS.items()}.get(picked, "?")
     return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "ramp": ramp,
             "ref_ms": ref_ms, "ref_tflops": prob.flops() / (ref_ms * 1e-3) / 1e12, "host": host, "form": form,

@@ -27,7 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "VARIANT_SHORT", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
+    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
@@ -121,11 +121,13 @@ def load_library(path=LIB_PATH):
 
 VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT, VARIANT_BALANCED = 0, 1, 2, 3, 4, 5
 VARIANT_SHORT = 6
+VARIANT_BALANCED_PAIR = 7  # the balanced form over M-tile pairs (a workspace, like VARIANT_BALANCED)
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
-            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT}
+            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
+            "balanced_pair": VARIANT_BALANCED_PAIR}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
@@ -151,8 +153,8 @@ def fmha_fwd_d64_bf16_ws(params, batch, causal, workspace=None, workspace_bytes=
     """The launch with a workspace (device pointer as int, 256-byte aligned,
     at least :func:`workspace_size` bytes; None with 0 bytes allowed), which
     lets dense causal launches with few heavy M-tiles run the balanced form.
-    ``variant``: VARIANT_AUTO, VARIANT_BALANCED or any other (workspace
-    unused).  Raises :class:`FmhaError` on a non-zero hipError_t."""
+    ``variant``: VARIANT_AUTO, VARIANT_BALANCED, VARIANT_BALANCED_PAIR or any
+    other (workspace unused).  Raises :class:`FmhaError` on a non-zero hipError_t."""
     rc = load_library().fmha_fwd_d64_bf16_ws(ctypes.byref(params), int(batch), int(causal), int(variant), workspace,
                                              int(workspace_bytes), stream)
     if rc != HIP_SUCCESS:
@@ -168,19 +170,24 @@ def workspace_size(params, batch, causal, variant=VARIANT_AUTO):
 
 def balanced_plan(params, batch, causal, compute_units=0, force=False):
     """(items, split_from) of the balanced form's plan: items per (batch,
-    head) in dispatch order as (M-tile, half) pairs, half None for a whole
-    M-tile; ([], None) when the launch would not be balanced.  Host only."""
+    head) in dispatch order as (unit, half) pairs, half None for a whole
+    unit; ([], None) when the launch would not be balanced.  ``force``: False
+    (the automatic rule), True (over M-tiles, as VARIANT_BALANCED) or "pair"
+    (over M-tile pairs, as VARIANT_BALANCED_PAIR: unit u is M-tiles 2u and
+    2u+1).  split_from counts M-tiles.  Host only."""
+    pair = force == "pair"
     cap = 4096
     buf = (ctypes.c_uint16 * cap)()
     sf = ctypes.c_int(-1)
     n = load_library().fmha_fwd_d64_bf16_balanced_plan(ctypes.byref(params), int(batch), int(causal),
-                                                       int(compute_units), int(bool(force)), buf, cap,
+                                                       int(compute_units), 2 if pair else int(bool(force)), buf, cap,
                                                        ctypes.byref(sf))
     if n < 0:
         raise FmhaError(HIP_ERROR_INVALID_VALUE, "fmha_fwd_d64_bf16_balanced_plan")
     if n == 0:
         return [], None
-    items = [(v & 0x7FFF, (v >> 15) if (v & 0x7FFF) >= sf.value else None) for v in buf[:n]]
+    first = 2 if pair else 1  # M-tiles per unit
+    items = [(v & 0x7FFF, (v >> 15) if first * (v & 0x7FFF) >= sf.value else None) for v in buf[:n]]
     return items, sf.value
 
 

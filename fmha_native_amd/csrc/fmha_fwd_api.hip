@@ -207,20 +207,23 @@ int causal_ntiles(const FmhaFwdParams* p, int mt) {
 // per resident block (otherwise the regular heaviest-first order balances
 // already).  Returns false when there is no plan (not causal dense, too many
 // items for the table); fills `a` (table, split range) when given.
-bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force,
+// How a plan is chosen: the automatic rule, or forced over single M-tiles
+// (FMHA_VARIANT_BALANCED) or over M-tile pairs (FMHA_VARIANT_BALANCED_PAIR).
+enum PlanMode : int { kPlanAuto = 0, kPlanSingle = 1, kPlanPair = 2 };
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode,
                          FmhaBalancedArgs* a, int64_t* ws_bytes);
 
 // The plan depends on the launch's shape only, so the last one built on a
 // thread is kept: a serving loop relaunching one shape skips the sort (about
 // 10 us of host time for cfg5's 531 items).
-bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force, FmhaBalancedArgs* a,
+bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode, FmhaBalancedArgs* a,
                    int64_t* ws_bytes) {
     struct Key {
-        int seqlen_q, seqlen_k, nhead_q, batch, causal, varlen, force;
+        int seqlen_q, seqlen_k, nhead_q, batch, causal, varlen, mode;
         int64_t cus;
         bool operator==(const Key& o) const {
             return seqlen_q == o.seqlen_q && seqlen_k == o.seqlen_k && nhead_q == o.nhead_q && batch == o.batch &&
-                   causal == o.causal && varlen == o.varlen && force == o.force && cus == o.cus;
+                   causal == o.causal && varlen == o.varlen && mode == o.mode && cus == o.cus;
         }
     };
     thread_local Key last_key{-1, -1, -1, -1, -1, -1, -1, -1};
@@ -228,9 +231,9 @@ bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, b
     thread_local int64_t last_bytes = 0;
     thread_local FmhaBalancedArgs last_plan;
     const Key key{p->seqlen_q, p->seqlen_k, p->nhead_q, batch, causal, p->seqstart_q != nullptr ? 1 : 0,
-                  force ? 1 : 0, cus};
+                  mode, cus};
     if (!(key == last_key)) {
-        last_ok = balanced_plan_build(p, batch, causal, cus, force, &last_plan, &last_bytes);
+        last_ok = balanced_plan_build(p, batch, causal, cus, mode, &last_plan, &last_bytes);
         last_key = key;
     }
     if (!last_ok) return false;
@@ -239,7 +242,7 @@ bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, b
         a->split_from = last_plan.split_from;
         a->n_split = last_plan.n_split;
         a->n_items = last_plan.n_items;
-        a->pad = 0;
+        a->pair = last_plan.pair;
         std::copy(last_plan.item, last_plan.item + last_plan.n_items, a->item);
     }
     return true;
@@ -270,7 +273,7 @@ bool balanced_pays(int64_t blocks, int heaviest, double avg, int64_t cus) {
     return heaviest >= 128 && heaviest > 1.5 * avg;
 }
 
-bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, bool force,
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode,
                          FmhaBalancedArgs* a, int64_t* ws_bytes) {
     if (!causal || p->seqstart_q != nullptr || batch <= 0 || p->seqlen_q <= 0 || cus <= 0) return false;
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
@@ -278,14 +281,31 @@ bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t 
     double total = 0.0;
     for (int mt = 0; mt < m_tiles; ++mt) total += causal_ntiles(p, mt);
     total *= (double)p->nhead_q * batch;
-    const double avg = total / (2.0 * (double)cus);  // key tiles per resident block
     const int heaviest = causal_ntiles(p, m_tiles - 1);
-    if (!force && !balanced_pays((int64_t)m_tiles * p->nhead_q * batch, heaviest, avg, cus)) return false;
-    const double limit = std::max(2.0, avg / 2);
-    int split_from = m_tiles;  // key tiles grow with the M-tile: the split ones are a suffix
-    while (split_from > 0 && causal_ntiles(p, split_from - 1) > limit) --split_from;
+    if (mode == kPlanAuto &&
+        !balanced_pays((int64_t)m_tiles * p->nhead_q * batch, heaviest, total / (2.0 * (double)cus), cus))
+        return false;
+    // work units: M-tiles (two resident blocks per CU) or M-tile pairs (one
+    // 8-wave block per CU), each unit's key tiles those of its last M-tile
+    const bool pair = mode == kPlanPair;
+    const int units = pair ? (m_tiles + 1) / 2 : m_tiles;
+    auto work = [&](int u) { return causal_ntiles(p, pair ? std::min(2 * u + 1, m_tiles - 1) : u); };
+    double unit_total = total;
+    if (pair) {
+        unit_total = 0.0;
+        for (int u = 0; u < units; ++u) unit_total += work(u);
+        unit_total *= (double)p->nhead_q * batch;
+    }
+    // key tiles per resident block (two per CU; a pair block alone on its CU)
+    const double avg = unit_total / ((pair ? 1.0 : 2.0) * (double)cus);
+    // units with more key tiles than this are split: half the average (pairs:
+    // 0.7 of it; B1 H2 S40000 causal measured 0.6-0.7 best, 0.5 -4 %, 1.0 -25 %)
+    const double limit = std::max(2.0, avg * (pair ? 0.7 : 0.5));
+    int split_u = units;  // key tiles grow with the unit: the split ones are a suffix
+    while (split_u > 0 && work(split_u - 1) > limit) --split_u;
+    const int split_from = pair ? std::min(2 * split_u, m_tiles) : split_u;
     const int n_split = m_tiles - split_from;
-    const int n_items = split_from + 2 * n_split;
+    const int n_items = split_u + 2 * (units - split_u);
     if (n_items > FMHA_BALANCED_MAX_ITEMS) return false;
     if (ws_bytes) *ws_bytes = (int64_t)n_split * p->nhead_q * batch * 2 * FMHA_BALANCED_PART_BYTES;
     if (a) {
@@ -293,31 +313,39 @@ bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t 
         // allocation-free entry point runs it too); the order is total, so
         // std::sort needs no stability
         struct It {
-            int w, mt, half;
+            int w, u, half;
         };
         It items[FMHA_BALANCED_MAX_ITEMS];
         int n = 0;
-        for (int mt = 0; mt < m_tiles; ++mt) {
-            const int kt = causal_ntiles(p, mt);
-            if (mt < split_from) {
-                items[n++] = {kt, mt, 0};
+        for (int u = 0; u < units; ++u) {
+            const int kt = work(u);
+            if (u < split_u) {
+                items[n++] = {kt, u, 0};
             } else {
-                items[n++] = {(kt + 1) / 2, mt, 0};
-                items[n++] = {kt / 2, mt, 1};
+                items[n++] = {(kt + 1) / 2, u, 0};
+                items[n++] = {kt / 2, u, 1};
             }
         }
         std::sort(items, items + n, [](const It& x, const It& y) {
             if (x.w != y.w) return x.w > y.w;
-            if (x.mt != y.mt) return x.mt > y.mt;
+            if (x.u != y.u) return x.u > y.u;
             return x.half < y.half;
         });
-        for (int i = 0; i < n_items; ++i) a->item[i] = (unsigned short)(items[i].mt | (items[i].half << 15));
+        for (int i = 0; i < n_items; ++i) a->item[i] = (unsigned short)(items[i].u | (items[i].half << 15));
         a->split_from = split_from;
         a->n_split = n_split;
         a->n_items = n_items;
-        a->pad = 0;
+        a->pair = pair ? 1 : 0;
     }
     return true;
+}
+
+// The plan mode of a variant that takes a workspace, or -1 for the others.
+int plan_mode(int v) {
+    return v == FMHA_VARIANT_AUTO            ? kPlanAuto
+           : v == FMHA_VARIANT_BALANCED      ? kPlanSingle
+           : v == FMHA_VARIANT_BALANCED_PAIR ? kPlanPair
+                                             : -1;
 }
 
 }  // namespace
@@ -325,8 +353,9 @@ bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t 
 extern "C" int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* p, int batch, int causal, int compute_units,
                                                int force, unsigned short* items, int capacity, int* split_from) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
+    if (force < kPlanAuto || force > kPlanPair) return -1;
     FmhaBalancedArgs a;
-    if (!balanced_plan(p, batch, causal, compute_units > 0 ? compute_units : device_cus(), force != 0, &a, nullptr))
+    if (!balanced_plan(p, batch, causal, compute_units > 0 ? compute_units : device_cus(), force, &a, nullptr))
         return 0;
     if (items != nullptr)
         for (int i = 0; i < a.n_items && i < capacity; ++i) items[i] = a.item[i];
@@ -336,10 +365,10 @@ extern "C" int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* p, int batch
 
 extern "C" int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* p, int batch, int causal, int variant) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
-    const int v = variant & ~FMHA_VARIANT_REFERENCE_ORDER;
-    if (v != FMHA_VARIANT_AUTO && v != FMHA_VARIANT_BALANCED) return 0;
+    const int mode = plan_mode(variant & ~FMHA_VARIANT_REFERENCE_ORDER);
+    if (mode < 0) return 0;
     int64_t bytes = 0;
-    if (!balanced_plan(p, batch, causal, device_cus(), v == FMHA_VARIANT_BALANCED, nullptr, &bytes)) return 0;
+    if (!balanced_plan(p, batch, causal, device_cus(), mode, nullptr, &bytes)) return 0;
     return bytes;
 }
 
@@ -347,22 +376,25 @@ extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, in
                                            void* workspace, int64_t workspace_bytes, hipStream_t stream) {
     const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
     if (chk != hipSuccess) return chk;
-    const int v = variant & ~FMHA_VARIANT_REFERENCE_ORDER;
-    if (v != FMHA_VARIANT_AUTO && v != FMHA_VARIANT_BALANCED)
-        return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
+    const int mode = plan_mode(variant & ~FMHA_VARIANT_REFERENCE_ORDER);
+    if (mode < 0) return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
     if (workspace_bytes < 0 || (workspace == nullptr && workspace_bytes != 0) ||
         (reinterpret_cast<uintptr_t>(workspace) & 255u))
         return hipErrorInvalidValue;
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;
     FmhaBalancedArgs a;
     int64_t need = 0;
-    const bool plan = balanced_plan(p, batch, causal, device_cus(), v == FMHA_VARIANT_BALANCED, &a, &need);
-    if (v == FMHA_VARIANT_BALANCED && (!plan || need > workspace_bytes)) return hipErrorInvalidValue;
+    const bool plan = balanced_plan(p, batch, causal, device_cus(), mode, &a, &need);
+    if (mode != kPlanAuto && (!plan || need > workspace_bytes)) return hipErrorInvalidValue;
     if (!plan || need > workspace_bytes) return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
     a.p = *p;
     a.part = (float*)workspace;
-    hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_msk1, dim3(p->nhead_q, batch, a.n_items), dim3(kBlockSize), 0,
-                       stream, a);
+    if (a.pair)
+        hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_pair_msk1, dim3(p->nhead_q, batch, a.n_items),
+                           dim3(FMHA_SPLIT_KBLOCK), 0, stream, a);
+    else
+        hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_msk1, dim3(p->nhead_q, batch, a.n_items), dim3(kBlockSize), 0,
+                           stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n_split == 0) return e;
     hipLaunchKernelGGL(fmha_fwd_d64_bf16_balanced_merge, dim3(p->nhead_q, a.n_split, batch), dim3(kBlockSize), 0,

@@ -232,7 +232,10 @@ struct Softmax {
 //  * kModeBalanced: one group, one item of a balanced causal launch: the
 //    whole M-tile, or one half of its key tiles (a split M-tile), whose
 //    partial result goes to a workspace slot for the merge launch.
-enum : int { kModeRegular = 0, kModeSplitKV = 1, kModePair = 2, kModeBalanced = 3 };
+//  * kModeBalancedPair: kModePair's two groups on one item of a balanced
+//    causal launch of M-tile pairs: the pair's key tiles, or one half of
+//    them, each group's partial result to its own M-tile's slot.
+enum : int { kModeRegular = 0, kModeSplitKV = 1, kModePair = 2, kModeBalanced = 3, kModeBalancedPair = 4 };
 // The key range of a balanced-launch item: `part` null for a whole M-tile;
 // otherwise half `half` of its key tiles and the slot of its partial result.
 struct Chunk {
@@ -244,7 +247,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
                                           Chunk ck = Chunk{0, nullptr}) {
     constexpr int kGroups = (kMode == kModeRegular || kMode == kModeBalanced) ? 1 : 2;
     constexpr bool kSplitKV = kMode == kModeSplitKV;
-    constexpr bool kPair = kMode == kModePair;
+    constexpr bool kPair = kMode == kModePair || kMode == kModeBalancedPair;
+    constexpr bool kBalanced = kMode == kModeBalanced || kMode == kModeBalancedPair;
     constexpr int kLoads = kPair ? 1 : kLoadsPerTile;  // DMA loads per wave, tensor and tile
     const int lane = threadIdx.x & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -309,8 +313,8 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     // below count group-local tiles 0 .. ntg-1); tiles >= tile_end are dead
     int ntg = kSplitKV ? (ntiles + 1) / 2 : ntiles;
     int tile0 = kSplitKV ? group * ntg : 0;
-    if constexpr (kMode == kModeBalanced) {
-        if (ck.part != nullptr) {  // a split M-tile: the first ceil(n/2) key tiles, or the rest
+    if constexpr (kBalanced) {
+        if (ck.part != nullptr) {  // a split M-tile (pair): the first ceil(n/2) key tiles, or the rest
             const int h0 = (ntiles + 1) / 2;
             tile0 = ck.half ? h0 : 0;
             ntg = ck.half ? ntiles - h0 : h0;
@@ -640,13 +644,16 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         sm.m_ref = m;
     }
 
-    if constexpr (kMode == kModeBalanced) {
+    if constexpr (kBalanced) {
         // a split M-tile's half: its unnormalised O^T, reference max and partial
         // row sums, lane-major (element e of lane L of wave w at
         // part[(34w + e) * 64 + L]: every store writes 256 contiguous bytes);
-        // the merge launch finishes the M-tile
+        // the merge launch finishes the M-tile.  A pair's second group writes
+        // the slot of M-tile 2mt+1 (two slots on: each M-tile holds its two
+        // halves), unless that M-tile is past the sequence.
         if (ck.part != nullptr) {
-            float* w = ck.part + wave * kPartFloatsPerWave;
+            if (kPair && row0 >= sq) return;
+            float* w = ck.part + group * (2 * kWaves * kPartFloatsPerWave) + wave * kPartFloatsPerWave;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -1691,6 +1698,15 @@ FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_balanced_msk1(FmhaBalancedArgs args) {
     const int mt = it & 0x7fff, half = it >> 15;
     const int b = blockIdx.y, h = blockIdx.x;
     fwd_mtile<true, false, kModeBalanced>(args.p, b, h, mt, ring, balanced_chunk(args, b, h, mt, half));
+}
+// The same over M-tile pairs (2*kBlockSize threads): item = pair | half << 15;
+// split_from is even, so a split pair's M-tiles are both split.
+FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_balanced_pair_msk1(FmhaBalancedArgs args) {
+    FMHA_RING(ring, kTileBytes)
+    const int it = args.item[blockIdx.z];
+    const int pr = it & 0x7fff, half = it >> 15;
+    const int b = blockIdx.y, h = blockIdx.x;
+    fwd_mtile<true, false, kModeBalancedPair>(args.p, b, h, pr, ring, balanced_chunk(args, b, h, 2 * pr, half));
 }
 
 // Merge of the two halves of a split M-tile (grid (nhead_q, n_split, batch)):

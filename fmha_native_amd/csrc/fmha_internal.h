@@ -38,9 +38,10 @@ struct FmhaBalancedArgs {
     int split_from;  // M-tiles >= split_from are split in two key halves
     int n_split;     // split M-tiles per (batch, head): m_tiles - split_from
     int n_items;     // items per (batch, head) (the grid's z)
-    int pad;
-    unsigned short item[FMHA_BALANCED_MAX_ITEMS];  // dispatch order: M-tile | half << 15
+    int pair;        // items are M-tile pairs (the pair entry, FMHA_SPLIT_KBLOCK threads)
+    unsigned short item[FMHA_BALANCED_MAX_ITEMS];  // dispatch order: M-tile (pair) | half << 15
 };
 
 __global__ void fmha_fwd_d64_bf16_balanced_msk1(FmhaBalancedArgs args);
+__global__ void fmha_fwd_d64_bf16_balanced_pair_msk1(FmhaBalancedArgs args);
 __global__ void fmha_fwd_d64_bf16_balanced_merge(FmhaBalancedArgs args);

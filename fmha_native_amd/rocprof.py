@@ -36,8 +36,9 @@ profiles other workloads in the kernel forms named (``auto`` = the
 launcher's choice; a form the launcher did not pick, beside it, shows what
 the choice gains): per workload and form, ``bench.py --only`` unprofiled, a
 kernel trace of every kernel of a step (the balanced causal form is two: its
-items, then the merge of its split M-tiles) and the utilisation counters of
-each kernel, with the clock from the same dispatches.
+items, then the merge of its split M-tiles), the utilisation counters of
+each kernel, with the clock from the same dispatches, and each kernel's HBM
+traffic (FETCH_SIZE and WRITE_SIZE passes, scaled by a device copy's).
 
     python -m fmha_native_amd.rocprof --short --summary profiles/NAME.md
 
@@ -191,6 +192,17 @@ def profile_forms(args):
           "(4·B·H·Sq·Sk·64, ×0.5 causal; varlen counts max(S) for every sequence, and the exact count of "
           "visible (q, k) pairs is given beside it).", ""]
     fig = {"made_by": f"python -m fmha_native_amd.rocprof --forms {args.forms}", "forms": {}}
+    # the counters' scale, from a device copy of known size (as the main run)
+    copy = {}
+    copy_cmds = []
+    for name, counter in (("pmc_copy_fetch", "FETCH_SIZE"), ("pmc_copy_write", "WRITE_SIZE")):
+        db, _l, cmd = _run(name, ["--pmc", counter], _bench("--copy-probe-mib", "256", "--steps", "5"), args.out, 120)
+        copy_cmds.append(cmd)
+        copy[counter] = 256 * 1024 / max(v[counter] for v in _counters(db, kernel_prefix="").values())
+    md += [f"HBM traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, each in a pass of its own) scaled by what "
+           f"each reads for a 256 MiB device copy (x{copy['FETCH_SIZE']:.3f}, x{copy['WRITE_SIZE']:.3f}), against "
+           "the algorithmic bytes (Q, K, V read once, O and LSE written once):", ""]
+    md += [f"    {c}" for c in copy_cmds] + [""]
     for spec in args.forms.split(","):
         wl, form = spec.split(":")
         prob, _mult = probs[wl]
@@ -215,6 +227,15 @@ def profile_forms(args):
                              _bench("--only", wl, "--variant", form, "--steps", "5", "--warmup", "1"), args.out, 120)
         cs = _counters(udb)
         n_se = _num_se(udb)
+        traffic, tcmds = {}, []
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            tdb, _l, c2 = _run(f"pmc_{counter.split('_')[0].lower()}_{tag}", ["--pmc", counter],
+                               _bench("--only", wl, "--variant", form, "--steps", "5", "--warmup", "1"), args.out, 120)
+            tcmds.append(c2)
+            for kname, v in _counters(tdb).items():
+                traffic.setdefault(kname, {})[counter] = v[counter] * copy[counter] * 1024
+        hbm = sum(t.get("FETCH_SIZE", 0) + t.get("WRITE_SIZE", 0) for t in traffic.values())
+        alg = prob.io_bytes()
         flops = prob.flops()
         md += [f"## {wl} ({prob.name}), form `{form}` → {line['form']}", "",
                f"bench.py (back-to-back HIP events): {line['ms_per_step'] * 1e3:.2f} us per step, "
@@ -249,9 +270,16 @@ def profile_forms(args):
                    "20 us); VGPR as rocprofv3 records it (4 registers per granule where gfx950 wave64 allocates 8: "
                    "128 shown = 256 allocated).", "",
                f"Kernel-trace time per step (sum of the kernels' averages): {step_us:.2f} us = "
-                   f"{flops / (step_us * 1e-6) / 1e12:.1f} TFLOP/s.", "", "Commands:", "",
+                   f"{flops / (step_us * 1e-6) / 1e12:.1f} TFLOP/s.", "",
+               "HBM traffic per step: " + "; ".join(
+                   f"`{k.split('(')[0]}` fetch {t.get('FETCH_SIZE', 0) / 1e6:.1f} MB, write "
+                   f"{t.get('WRITE_SIZE', 0) / 1e6:.1f} MB" for k, t in sorted(traffic.items()))
+               + f"; total {hbm / 1e6:.1f} MB against {alg / 1e6:.1f} MB algorithmic ({hbm / alg:.2f}x).", "",
+               "Commands:", "",
                f"    python3 bench.py --only {wl} --variant {form} --steps {steps} --warmup 5",
-               f"    {tcmd}", f"    {ucmd}", ""]
+               f"    {tcmd}", f"    {ucmd}"] + [f"    {c}" for c in tcmds] + [""]
+        entry["traffic"] = {"hbm_bytes": int(hbm), "algorithmic_bytes": int(alg),
+                            "kernels": {k: {c: int(v) for c, v in t.items()} for k, t in traffic.items()}}
         fig["forms"][tag] = entry
     path = args.summary or os.path.join(args.out, "forms.md")
     with open(path, "w") as f:

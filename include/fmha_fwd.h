@@ -152,6 +152,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_PERSISTENT 4
 #define FMHA_VARIANT_BALANCED 5 /* fmha_fwd_d64_bf16_ws only: it needs a workspace */
 #define FMHA_VARIANT_SHORT 6
+#define FMHA_VARIANT_BALANCED_PAIR 7 /* fmha_fwd_d64_bf16_ws only: the balanced form over M-tile pairs */
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
@@ -175,7 +176,11 @@ hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int
  *            FMHA_VARIANT_BALANCED (always the balanced form, with the
  *            heavy-M-tile rule applied even where the regular order would
  *            balance: causal dense only; hipErrorInvalidValue if it cannot
- *            run), or any other variant (workspace unused, as
+ *            run), FMHA_VARIANT_BALANCED_PAIR (the same over M-tile pairs in
+ *            8-wave blocks, one per compute unit: pairs above 0.7 of the
+ *            average work per unit are split; a group's partial goes to its
+ *            own M-tile's slot, so the workspace size is the same formula),
+ *            or any other variant (workspace unused, as
  *            fmha_fwd_d64_bf16_variant).
  *   workspace: device memory, 256-byte aligned, at least
  *            fmha_fwd_d64_bf16_workspace_size() bytes, or NULL with 0 bytes
@@ -205,10 +210,11 @@ hipError_t fmha_fwd_d64_bf16_noalloc(const FmhaFwdParams* params, int batch, int
                                      hipStream_t stream);
 
 /* The balanced form's plan for these arguments on a device with
- * `compute_units` compute units (0 = the current device's; `force` as
- * FMHA_VARIANT_BALANCED): writes up to `capacity` items (dispatch order;
- * M-tile | half << 15, half 0 = the first ceil(n/2) key tiles) and the first
- * split M-tile, and returns the number of items per (batch, head); 0 when
+ * `compute_units` compute units (0 = the current device's; `force` 0: the
+ * automatic rule, 1: as FMHA_VARIANT_BALANCED, 2: as
+ * FMHA_VARIANT_BALANCED_PAIR, whose items are M-tile pairs): writes up to
+ * `capacity` items (dispatch order; M-tile (pair) | half << 15, half 0 = the
+ * first ceil(n/2) key tiles) and the first split M-tile (even for pairs), and returns the number of items per (batch, head); 0 when
  * the launch would not be balanced, -1 for rejected arguments.  Host only
  * (this build's own; no counterpart in the reference). */
 int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* params, int batch, int causal, int compute_units, int force,

@@ -71,6 +71,50 @@ def test_balanced_equals_splitkv_and_regular_per_mtile(b, h, hk, sq, sk, lse, mu
         assert verify.lse_rule(l_ref, lb)["pass"]
 
 
+@pytest.mark.parametrize("b,h,hk,sq,sk,lse,mult", [
+    (1, 2, 2, 40000, 40000, True, 2.0),   # the benchmark configuration: 313 M-tiles, an odd last pair
+    (1, 2, 1, 5000, 5000, True, 1.0),
+    (2, 4, 2, 3000, 3500, True, 1.0),     # Sk > Sq, GQA, two batches
+    (1, 3, 1, 2000, 1500, False, 1.0),    # Sq > Sk: the first rows see no key
+    (3, 2, 2, 700, 700, True, 1.0),
+    (1, 2, 2, 8192, 8192, True, 1.0),     # an even M-tile count
+])
+def test_balanced_pair_equals_pair_and_splitkv_per_mtile(b, h, hk, sq, sk, lse, mult):
+    """The balanced form over M-tile pairs: a whole pair runs the pair form's
+    code path (bits equal the pair form's); a split pair's second M-tile has
+    the pair's key tiles, so its two halves are the split-KV form's (bits
+    equal); its first M-tile's halves differ from the split-KV form's (the
+    pair's two extra, masked, key tiles shift the cut), so those rows meet the
+    rule against the oracle, as every row does."""
+    import torch
+
+    prob = Problem(batch=b, nhead_q=h, nhead_k=hk, seqlen_q=sq, seqlen_k=sk, causal=True, lse=lse)
+    nq, nk, nlse = prob.sizes()
+    host = [torch.empty(n, dtype=torch.int16) for n in (nq, nk, nk, nq)]
+    p = build_params(prob, *host, torch.empty(max(nlse, 1), dtype=torch.float32) if lse else None, None)
+    items, sf = fmha.balanced_plan(p, prob.batch, 1, 0, force="pair")
+    assert items
+    q, k, v = make_inputs(prob, "normal", 64, mult)
+    ob, lb = run_kernel(prob, q, k, v, variant=fmha.VARIANT_BALANCED_PAIR)
+    op, lp = run_kernel(prob, q, k, v, variant=fmha.VARIANT_PAIR)
+    os_, ls = run_kernel(prob, q, k, v, variant=fmha.VARIANT_SPLITKV)
+    mt = np.arange(sq) // 128
+    split = mt >= sf
+    odd = split & (mt % 2 == 1)
+    print(f"split_from {sf}: {split.sum()} of {sq} rows in split M-tiles", flush=True)
+    o3 = [x.reshape(b, h, sq, 64) for x in (ob, op, os_)]
+    assert np.array_equal(o3[0][:, :, ~split], o3[1][:, :, ~split])
+    assert np.array_equal(o3[0][:, :, odd], o3[2][:, :, odd])
+    if lse:
+        l3 = [x.reshape(b, h, sq) for x in (lb, lp, ls)]
+        assert np.array_equal(l3[0][:, :, ~split], l3[1][:, :, ~split])
+        assert np.array_equal(l3[0][:, :, odd], l3[2][:, :, odd])
+    o_ref, l_ref = oracle.run(prob, q, k, v, p_trunc=False)
+    assert verify.baseline_rule(o_ref, verify.bf16_bits_to_f32(ob))["pass"]
+    if lse:
+        assert verify.lse_rule(l_ref, lb)["pass"]
+
+
 def test_auto_takes_balanced_with_a_workspace_and_reuses_it():
     """B1 H2 S40000 causal: the automatic choice with a workspace is the
     balanced form (its bits equal the forced balanced launch's); a second

@@ -383,6 +383,38 @@ def test_balanced_plan_is_longest_first_over_every_key_tile(b, h, sq, sk, cus, f
         assert ws == (m_tiles - sf) * h * b * 2 * 4 * 34 * 64 * 4
 
 
+@pytest.mark.parametrize("b,h,sq,sk,cus", [
+    (1, 2, 40000, 40000, 256),   # cfg5: 313 M-tiles, an odd last pair
+    (1, 2, 40064, 40064, 256),   # 313 M-tiles, the last one full
+    (2, 3, 3000, 3500, 256),
+    (1, 1, 300, 200, 256),       # one pair, not split
+    (1, 4, 8192, 8192, 64),
+])
+def test_balanced_pair_plan_covers_every_pair_once(b, h, sq, sk, cus):
+    """The plan over M-tile pairs (one 8-wave block per compute unit): unit u
+    is M-tiles 2u and 2u+1 with the key tiles of the later one; whole units
+    below split_from / 2 and two halves from it on, in non-increasing order
+    of work; split_from is even (both M-tiles of a split pair are split) or
+    the M-tile count; the workspace holds two partials per split M-tile."""
+    p = valid_params(lse=False)
+    p.nhead_q, p.nhead_k, p.seqlen_q, p.seqlen_k = h, h, sq, sk
+    items, sf = fmha.balanced_plan(p, b, 1, cus, "pair")
+    m_tiles = -(-sq // 128)
+    units = (m_tiles + 1) // 2
+    n = [_ntiles(min(2 * u + 1, m_tiles - 1), sq, sk) for u in range(units)]
+    avg = sum(n) * h * b / cus
+    su = sum(1 for x in n if x <= max(2.0, 0.7 * avg))
+    assert all(x <= y for x, y in zip(n, n[1:]))
+    assert sf == min(2 * su, m_tiles) and (sf % 2 == 0 or sf == m_tiles)
+    expect = {(u, None) for u in range(su)} | {(u, half) for u in range(su, units) for half in (0, 1)}
+    assert len(items) == len(expect) and set(items) == expect
+    work = [n[u] if half is None else (n[u] + 1) // 2 if half == 0 else n[u] // 2 for u, half in items]
+    assert all(x >= y for x, y in zip(work, work[1:]))
+    if cus == 256:
+        ws = fmha.workspace_size(p, b, 1, fmha.VARIANT_BALANCED_PAIR)
+        assert ws == (m_tiles - sf) * h * b * 2 * 4 * 34 * 64 * 4
+
+
 @pytest.mark.parametrize("b,h,sq,causal", [(4, 16, 2048, 0), (4, 16, 2048, 1), (1, 16, 8192, 1), (1, 4, 32768, 1)])
 def test_balanced_plan_only_where_the_heaviest_m_tile_outlasts_the_average(b, h, sq, causal):
     p = valid_params(lse=False)
@@ -459,7 +491,8 @@ def test_ws_entry_rejects_bad_workspaces_and_forms():
                  (1, 1, B, None, 5),               # bytes without memory
                  (1, 1, B, ws, -1),
                  (1, 0, B, ws, need),              # not causal
-                 (1, 1, 99, ws, need)]:            # unknown form
+                 (1, 1, 99, ws, need),             # unknown form
+                 (1, 1, fmha.VARIANT_BALANCED_PAIR, ws, fmha.workspace_size(p, 1, 1, 7) - 1)]:
         assert lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), *args, None) == INVALID, args
     assert fmha.workspace_size(_mut(q=None), 1, 1) == -1
     assert fmha.workspace_size(p, 1, 1, fmha.VARIANT_REGULAR) == 0

@@ -50,7 +50,8 @@ def test_every_entry_compiled(asm):
         assert any(e + "13FmhaFwdParams" in n for n in names), e
     for m in (0, 1):
         assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
-    for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_merge"):
+    for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_pair_msk1",
+              "fmha_fwd_d64_bf16_balanced_merge"):
         assert any(e in n for n in names), e
     for m in (0, 1):
         for v in ("", "_varlen"):

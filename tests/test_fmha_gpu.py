@@ -42,14 +42,15 @@ FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair
          "persistent": fmha.VARIANT_PERSISTENT}
 # the balanced form (causal dense, through the workspace entry) runs on the
 # matrices of reference cases and benchmark configurations
-MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, short=fmha.VARIANT_SHORT)
+MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, balanced_pair=fmha.VARIANT_BALANCED_PAIR,
+                    short=fmha.VARIANT_SHORT)
 
 
 def _dense_only(form, prob):
     if form == "persistent" and prob.varlen:
         pytest.skip("the persistent form takes dense problems only")
-    if form == "balanced" and (prob.varlen or not prob.causal):
-        pytest.skip("the balanced form takes causal dense problems only")
+    if form.startswith("balanced") and (prob.varlen or not prob.causal):
+        pytest.skip("the balanced forms take causal dense problems only")
 
 
 @pytest.mark.parametrize("form", list(MATRIX_FORMS))

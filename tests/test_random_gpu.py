@@ -91,7 +91,8 @@ def test_wide_random_sweep():
 
     from harness import make_inputs, run_kernel
 
-    forms = dict(FORMS, auto=fmha.VARIANT_AUTO, balanced=fmha.VARIANT_BALANCED)
+    forms = dict(FORMS, auto=fmha.VARIANT_AUTO, balanced=fmha.VARIANT_BALANCED,
+                 balanced_pair=fmha.VARIANT_BALANCED_PAIR)
     failed = []
     runs = 0
     for i in range(400):
@@ -99,7 +100,8 @@ def test_wide_random_sweep():
         q, k, v = make_inputs(prob, "ref", 100 + i)
         o_ref, lse_ref = oracle.run(prob, q, k, v)
         for name, var in forms.items():
-            if (name == "persistent" and prob.varlen) or (name == "balanced" and (prob.varlen or not prob.causal)):
+            if (name == "persistent" and prob.varlen) or \
+                    (name.startswith("balanced") and (prob.varlen or not prob.causal)):
                 continue
             ob, lb = run_kernel(prob, q, k, v, variant=var)
             ok = verify.reference_rule(o_ref, verify.bf16_bits_to_f32(ob))["pass"]
