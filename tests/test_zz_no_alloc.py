@@ -26,7 +26,7 @@ def _need_gpu():
     fmha.load_library()
 
 
-def _launch(prob, q, k, v, noalloc):
+def _launch(prob, q, k, v, noalloc, variant=fmha.VARIANT_AUTO):
     import torch
 
     nq, nk, nlse = prob.sizes()
@@ -36,26 +36,27 @@ def _launch(prob, q, k, v, noalloc):
     p = build_params(prob, dq, dk, dv, do, dl, None)
     lib = fmha.load_library()
     if noalloc:
-        rc = lib.fmha_fwd_d64_bf16_noalloc(ctypes.byref(p), prob.batch, 1, fmha.VARIANT_AUTO, None)
+        rc = lib.fmha_fwd_d64_bf16_noalloc(ctypes.byref(p), prob.batch, 1, variant, None)
     else:
-        need = fmha.workspace_size(p, prob.batch, 1)
+        need = fmha.workspace_size(p, prob.batch, 1, variant)
         ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda:0")
-        rc = lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), prob.batch, 1, fmha.VARIANT_AUTO, ws.data_ptr(), need, None)
+        rc = lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), prob.batch, 1, variant, ws.data_ptr(), need, None)
     assert rc == 0, rc
     torch.cuda.synchronize()
     return do.cpu().numpy().view(np.uint16), dl.cpu().numpy()
 
 
-def test_no_alloc_equals_workspace_entry_on_two_calls():
+@pytest.mark.parametrize("variant", [fmha.VARIANT_AUTO, fmha.VARIANT_BALANCED_PAIR])
+def test_no_alloc_equals_workspace_entry_on_two_calls(variant):
     """Two calls in a row, the second on a smaller problem: the balanced form
-    (30.4 MB of partials, then 2.3 MB) from the static array gives the bits
-    the workspace entry gives."""
+    (30.4 MB of partials, then 2.3 MB; over M-tile pairs 24.9 MB, then less)
+    from the static array gives the bits the workspace entry gives."""
     for seq, heads, mult in ((40000, 2, 2.0), (16384, 2, 1.0)):
         prob = Problem(batch=1, nhead_q=heads, seqlen_q=seq, causal=True, lse=True)
         q, k, v = make_inputs(prob, "normal", 70 + heads, mult)
-        print(f"noalloc vs ws: B1 H{heads} S{seq} causal", flush=True)
-        o_ws, l_ws = _launch(prob, q, k, v, noalloc=False)
-        o_na, l_na = _launch(prob, q, k, v, noalloc=True)
+        print(f"noalloc vs ws (variant {variant}): B1 H{heads} S{seq} causal", flush=True)
+        o_ws, l_ws = _launch(prob, q, k, v, noalloc=False, variant=variant)
+        o_na, l_na = _launch(prob, q, k, v, noalloc=True, variant=variant)
         assert np.array_equal(o_na, o_ws)
         assert np.array_equal(l_na, l_ws)
 
