@@ -198,16 +198,18 @@ int causal_ntiles(const FmhaFwdParams* p, int mt) {
     return (kv_end + kN0 - 1) / kN0;
 }
 
-// Plan of a balanced causal launch on `cus` compute units (two resident
-// blocks each): the M-tiles whose key tiles exceed half the average work per
-// resident block are split into two key halves (so none outlasts the average
-// much), and the items are ordered by work, heaviest first (longest
-// processing time first; ties: later M-tile, first half).  Without `force`
-// the plan is taken only when the heaviest M-tile exceeds the average work
-// per resident block (otherwise the regular heaviest-first order balances
-// already).  Returns false when there is no plan (not causal dense, too many
-// items for the table); fills `a` (table, split range) when given.
-// How a plan is chosen: the automatic rule, or forced over single M-tiles
+// Plan of a balanced causal launch on `cus` compute units.  Work units are
+// M-tiles (two resident blocks per CU) or, in pair mode, M-tile pairs (one
+// 8-wave block per CU); the units whose key tiles exceed a fraction of the
+// average work per resident block (half; pairs 0.7) are split into two key
+// halves (so none outlasts the average much), and the items are ordered by
+// work, heaviest first (longest processing time first; ties: later unit,
+// first half).  In the automatic mode (over M-tiles) the plan is taken only
+// where balanced_pays() says it measured faster.  Returns false when there is
+// no plan (not causal dense, too many items for the table); fills `a` (table,
+// split range in M-tiles, pair flag) when given.
+//
+// Modes: the automatic rule, or forced over single M-tiles
 // (FMHA_VARIANT_BALANCED) or over M-tile pairs (FMHA_VARIANT_BALANCED_PAIR).
 enum PlanMode : int { kPlanAuto = 0, kPlanSingle = 1, kPlanPair = 2 };
 bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode,
