@@ -548,6 +548,52 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
     using No = std::false_type;
     auto mid = [&](int t, auto phase_c) { iteration(t, phase_c, Yes{}, Yes{}); };
 
+    // Causal: tiles past the last key this wave's rows can see hold only
+    // masked scores for it (P = 0; the pair form's first group has two such
+    // tiles at the end, every M-tile's first two waves one).  The wave
+    // computes its live tiles only and then keeps the ring going without
+    // compute: each later iteration still waits for its own loads, passes
+    // the barrier and issues its share of the DMA, so every wave passes the
+    // same barriers and issues the same loads as before.
+    int nlive = ntg;
+    if constexpr (kCausal) {
+        const int last_key = min(sk - 1, wrow0 + kRowsPerWave - 1 + shift);
+        const int lt = last_key < 0 ? 0 : last_key / kTileN + 1 - tile0;  // local tiles up to that key
+        nlive = max(1, min(ntg, lt));
+    }
+    // iteration t of a wave past its live tiles (phase J): its loads, and
+    // the GEMM1 of its last live tile when kG1
+    auto idle = [&](int t, auto phase_c, auto g1_c) {
+        constexpr int J = decltype(phase_c)::value;
+        vmcnt_wait<4 * kLoads>();
+        ring_barrier();
+        issue_k(t + kRing, std::integral_constant<int, J>{});
+        issue_v(t + 2, std::integral_constant<int, (J + 2) % kRing>{});
+        if constexpr (decltype(g1_c)::value)
+            gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[(J & 1) ^ 1]);
+    };
+    // after the last live tile (phase J): the block's last GEMM1, or the
+    // idle iterations up to ntg and the block's final barrier
+    auto finish_live = [&](auto phase_c) {
+        constexpr int J = decltype(phase_c)::value;
+        if (nlive == ntg) {
+            last_gemm1(phase_c);
+            return;
+        }
+        idle(nlive, std::integral_constant<int, (J + 1) % kRing>{}, Yes{});
+        for (int u = nlive + 1; u < ntg; u += kRing) {
+            idle(u, std::integral_constant<int, (J + 2) % kRing>{}, No{});
+            if (u + 1 >= ntg) break;
+            idle(u + 1, std::integral_constant<int, (J + 3) % kRing>{}, No{});
+            if (u + 2 >= ntg) break;
+            idle(u + 2, std::integral_constant<int, J>{}, No{});
+            if (u + 3 >= ntg) break;
+            idle(u + 3, std::integral_constant<int, (J + 1) % kRing>{}, No{});
+        }
+        vmcnt_wait<0>();  // every DMA landed (none may outlive the block)
+        ring_barrier();   // the other waves' last GEMM1 barrier
+    };
+
     if (ntg > 0) {
         // prologue: Q, then K0 K1 V0 K2 V1 K3 in flight; GEMM0 of tile 0 once
         // Q and K0 landed
@@ -585,14 +631,26 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
         // the next tile (for the last one a dead, zero-filled tile)
         iteration(0, P0{}, No{}, Yes{});
         int t = 1;
-        for (; t + kRing <= ntg; t += kRing) {
+        for (; t + kRing <= nlive; t += kRing) {
             mid(t, P1{});
             mid(t + 1, P2{});
             mid(t + 2, P3{});
             mid(t + 3, P0{});
         }
-        const int rem = ntg - t;
-        if (rem == 0) {
+        const int rem = nlive - t;  // 0-3 live tiles left; the last live tile's phase is rem
+        if constexpr (kCausal) {
+            // one shared tail after the live remainder (a copy of the
+            // live/idle tail per remainder, nested as below, spills)
+            if (rem >= 1) mid(t, P1{});
+            if (rem >= 2) mid(t + 1, P2{});
+            if (rem >= 3) mid(t + 2, P3{});
+            switch (rem) {
+                case 0: finish_live(P0{}); break;
+                case 1: finish_live(P1{}); break;
+                case 2: finish_live(P2{}); break;
+                default: finish_live(P3{}); break;
+            }
+        } else if (rem == 0) {  // every tile live; nested (0.9 % faster than the shared tail)
             last_gemm1(P0{});
         } else {
             mid(t, P1{});
