@@ -171,7 +171,9 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
 // us, causal S64 24.8 against 35.1 us); back to back, H16, 65,536-262,144 rows: 8-14 % faster dense at
 // 160-192 keys, 3 % at 224, -6 to +1 % at 256-320, 2-8 % slower at 384;
 // causal 12-21 % faster at 160-192 keys at every size, 7-11 % at 224-384
-// keys from 262,144 rows and -14 to +2 % below.  On smaller grids one
+// keys from 262,144 rows, 1-9 % at 229,376-258,048 rows (7 x CUs x 128; it
+// skips the key halves a wave cannot see) and -14 to +2 % below (S384 at
+// 196,608 rows -7 %; S512-S640 -5 to -6 % at any size).  On smaller grids one
 // block's latency sets the launch time and the regular form wins (B1 H2
 // S128: 4.6 against 5.6 us).  Varlen batches of 256-2048 sequences of 16-192
 // tokens, H16: 13-33 % faster.  Past a few key tiles the regular form's
@@ -181,7 +183,7 @@ int64_t pair_blocks(const FmhaFwdParams* p, int batch) {
 int pick_form(const FmhaFwdParams* p, int batch, int causal, int64_t cus) {
     const int64_t rows = (int64_t)batch * p->nhead_q * p->seqlen_q;
     if (p->seqlen_k <= kShortKeys && rows >= 2 * cus * kM0) return FMHA_VARIANT_SHORT;
-    if (causal && p->seqlen_k <= kShortKeysCausal && rows >= 8 * cus * kM0) return FMHA_VARIANT_SHORT;
+    if (causal && p->seqlen_k <= kShortKeysCausal && rows >= 7 * cus * kM0) return FMHA_VARIANT_SHORT;
     return pick_variant(grid_blocks(p, batch), pair_blocks(p, batch), causal, p->seqlen_k, cus);
 }
 

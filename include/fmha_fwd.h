@@ -116,7 +116,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *                         launches with seqlen_k <= 192 and at least
  *                         2 x CUs x 128 query rows (batch x nhead_q x
  *                         seqlen_q; varlen: the bounds), or causal with
- *                         seqlen_k <= 384 and at least 8 x CUs x 128; with
+ *                         seqlen_k <= 384 and at least 7 x CUs x 128; with
  *                         seqlen_k >= 2048,
  *                         split-KV when the regular grid has at most one
  *                         block per compute unit (causal: at most 1.5, or up

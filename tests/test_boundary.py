@@ -220,7 +220,7 @@ R, S, P = fmha.VARIANT_REGULAR, fmha.VARIANT_SPLITKV, fmha.VARIANT_PAIR
 def test_short_form_rule():
     """Launches whose keys fit three 64-key tiles take the short form once
     they hold two blocks' worth of query rows per compute unit (2 x CUs x 128
-    rows), causal ones with up to 384 keys once they hold eight; varlen ones
+    rows), causal ones with up to 384 keys once they hold seven; varlen ones
     by their bounds (batch x nhead_q x seqlen_q rows, seqlen_k keys: the
     short form reads each sequence's own lengths, so the bounds only steer
     the choice); smaller grids keep the grid-shape rule."""
@@ -230,8 +230,8 @@ def test_short_form_rule():
             (128, 127, 256, False, False), (128, 152, 304, True, True), (128, 151, 304, False, False),
             (128, 4096, 256, True, True),
             (129, 128, 256, True, True), (192, 128, 256, True, True), (192, 127, 256, False, False),
-            (193, 511, 256, False, False), (193, 512, 256, False, True), (384, 512, 256, False, True),
-            (384, 607, 304, False, False), (384, 608, 304, False, True), (385, 4096, 256, False, False),
+            (193, 447, 256, False, False), (193, 448, 256, False, True), (384, 448, 256, False, True),
+            (384, 531, 304, False, False), (384, 532, 304, False, True), (385, 4096, 256, False, False),
             (513, 4096, 256, False, False), (2048, 4096, 256, False, False)):
         for causal, short in ((0, dense), (1, causal_short)):
             got = fmha.pick_variant(_mut(seqlen_k=sk, lse=None), batch, causal, cus)
