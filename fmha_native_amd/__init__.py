@@ -27,7 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANT_PERSISTENT", "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
+    "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANTS",
 ]
 
@@ -119,14 +119,14 @@ def load_library(path=LIB_PATH):
     return lib
 
 
-VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_PERSISTENT, VARIANT_BALANCED = 0, 1, 2, 3, 4, 5
+VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_BALANCED = 0, 1, 2, 3, 5
 VARIANT_SHORT = 6
 VARIANT_BALANCED_PAIR = 7  # the balanced form over M-tile pairs (a workspace, like VARIANT_BALANCED)
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
-            "persistent": VARIANT_PERSISTENT, "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
+            "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
             "balanced_pair": VARIANT_BALANCED_PAIR}
 
 
@@ -135,8 +135,8 @@ def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):
 
     ``variant``: VARIANT_AUTO (the launcher's choice), VARIANT_REGULAR (the
     reference-named entries), VARIANT_SPLITKV (the split-KV entries),
-    VARIANT_PAIR (the pair entries) or VARIANT_PERSISTENT (dense only: blocks
-    looping over M-tiles), each optionally OR-ed with
+    VARIANT_PAIR (the pair entries) or VARIANT_SHORT (the short entries),
+    each optionally OR-ed with
     VARIANT_REFERENCE_ORDER (keep the reference's batch-after-batch block order
     for causal dense batches)."""
     lib = load_library()

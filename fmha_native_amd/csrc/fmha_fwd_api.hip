@@ -424,33 +424,14 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     if (chk != hipSuccess) return chk;
     const bool tile_major = (variant & FMHA_VARIANT_REFERENCE_ORDER) == 0 && use_tilemajor(p, batch, causal);
     variant &= ~FMHA_VARIANT_REFERENCE_ORDER;
-    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_BALANCED)
-        return hipErrorInvalidValue;  // the balanced form needs fmha_fwd_d64_bf16_ws
+    // the balanced forms need fmha_fwd_d64_bf16_ws; 4 is a retired value
+    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_BALANCED ||
+        variant == 4)
+        return hipErrorInvalidValue;
     const bool varlen = p->seqstart_q != nullptr;
-    if (variant == FMHA_VARIANT_PERSISTENT && varlen) return hipErrorInvalidValue;  // dense only
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
-    if (variant == FMHA_VARIANT_PERSISTENT) {
-        const int64_t items = (int64_t)p->nhead_q * m_tiles * batch;
-        const int64_t slots = 2 * (int64_t)device_cus();
-        if (items + slots >= INT32_MAX) return hipErrorInvalidValue;  // item numbers are ints
-        static std::atomic<unsigned> next_slot{0};
-        FmhaPersistArgs a;
-        a.p = *p;
-        a.queue = fmha_persist_queue_slot(next_slot.fetch_add(1, std::memory_order_relaxed));
-        if (a.queue == nullptr) return hipErrorInvalidSymbol;
-        a.batch = batch;
-        a.m_tiles = m_tiles;
-        a.n_items = (int)items;
-        a.tile_major = tile_major ? 1 : 0;
-        const dim3 pgrid((unsigned)(items < slots ? items : slots));
-        if (causal)
-            hipLaunchKernelGGL(fmha_fwd_d64_bf16_persist_msk1, pgrid, dim3(kBlockSize), 0, stream, a);
-        else
-            hipLaunchKernelGGL(fmha_fwd_d64_bf16_persist_msk0, pgrid, dim3(kBlockSize), 0, stream, a);
-        return hipGetLastError();
-    }
     if (variant == FMHA_VARIANT_AUTO)
         variant = pick_form(p, batch, causal, device_cus());
     if (variant == FMHA_VARIANT_SHORT) {

@@ -44,7 +44,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <atomic>
 #include <utility>
 
 #include "fmha_fwd.h"
@@ -785,548 +784,6 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 }
 
 // ===========================================================================
-// Persistent form (this build's own; no counterpart in the reference).
-//
-// One block per resident slot (2 per compute unit) loops over M-tile work
-// items until the queues run dry, so a block's K/V ring never drains between
-// items: the next item's first K/V tiles are fetched during the current
-// item's last iterations, its Q rows arrive by LDS-DMA into a buffer private
-// to each wave, its first GEMM0 runs in the current item's last iteration,
-// and the current item's last GEMM1 and its O/LSE epilogue run in the next
-// item's first iteration.  A regular launch instead pays, per block, the
-// latency of its first Q/K loads, a pipeline fill and drain, and an epilogue
-// with no MFMA work beside it.
-//
-// Items are the regular grid's blocks, numbered as the hardware would
-// dispatch them (head fastest); block j takes item j first, then items from
-// the queue of the XCD it runs on: queue x hands out the items >= gridDim.x
-// whose number is x mod 8, so (as in a regular launch, whose blocks go to the
-// XCDs round robin) all M-tiles of a head stay on one XCD and its K/V in that
-// XCD's L2.  Causal items come heaviest first.  Every item runs a multiple
-// of 4 ring iterations (the ring stages stay compile-time) and at least
-// kMinItemIters (room for the successor handover below); the padding
-// iterations see zero-filled, fully masked tiles.
-//
-// Successor handover, per item: wave 0 takes the next item number from the
-// queue with one atomic at iteration 0 (before that iteration's DMAs, so the
-// regular vmcnt waits retire it by iteration 2), writes it to the first word
-// of its Q buffer at iteration 2, and every wave reads it at iteration 3.  The
-// queue counters start at zero; the last block to finish resets them.
-// ===========================================================================
-constexpr int kQueues = 8;                                   // one item queue per XCD
-constexpr int kQueueStride = 32;                             // ints between counters: one 128-byte line each
-constexpr int kMinItemIters = 8;
-constexpr int kQBufBytes = kWaves * kRowsPerWave * kRowBytes;  // 16 KiB: each wave's 32 Q rows
-
-static_assert(kQueues == FMHA_PERSIST_QUEUES && kQueueStride == FMHA_PERSIST_QUEUE_STRIDE, "queue layout");
-using PersistArgs = FmhaPersistArgs;
-
-typedef __attribute__((address_space(4))) const PersistArgs* ArgsPtr;
-
-// The kernarg block through a pointer the compiler cannot follow across
-// calls of this function: loads through the result are issued where they
-// are used instead of being held in SGPRs across the inner loop.
-__device__ __forceinline__ ArgsPtr args_here() {
-    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(ap));
-    return ap;
-}
-
-// Where item L sits: batch b, head h, M-tile mt (wave-uniform).
-template <bool kCausal>
-__device__ __forceinline__ void item_coords(ArgsPtr ap, int L, int& b, int& h, int& mt) {
-    const int nh = ap->p.nhead_q;
-    h = L % nh;
-    const int r = L / nh;
-    int y;
-    if (kCausal && ap->tile_major) {
-        b = r % ap->batch;
-        y = r / ap->batch;
-    } else {
-        y = r % ap->m_tiles;
-        b = r / ap->m_tiles;
-    }
-    mt = kCausal ? ap->m_tiles - 1 - y : y;  // causal: heaviest M-tiles first
-}
-
-// What the K/V ring needs of an item (wave-uniform): the first K and V row of
-// its (batch, KV head), its first query row, its key tiles and its ring
-// iterations (key tiles rounded up to 4, at least kMinItemIters).  An item
-// number past the last is a dead item: no tiles (its loads are zero fills).
-struct ItemKV {
-    const char* k;
-    const char* v;
-    int row0;
-    int ntiles;
-    int npad;
-};
-template <bool kCausal>
-__device__ __forceinline__ ItemKV item_kv(ArgsPtr ap, int L) {
-    const bool valid = L < ap->n_items;
-    int b, h, mt;
-    item_coords<kCausal>(ap, valid ? L : 0, b, h, mt);
-    const int sq = ap->p.seqlen_q, sk = ap->p.seqlen_k;
-    int kv_end = sk;
-    if constexpr (kCausal) {  // pipeline.hpp:168-193, as the regular form
-        const int last = min(mt * kTileM + kTileM - 1, sq - 1);
-        const int e = last + (sk - sq) + 1;
-        kv_end = e < 0 ? 0 : (e > sk ? sk : e);
-    }
-    ItemKV it;
-    it.row0 = mt * kTileM;
-    it.ntiles = valid ? (kv_end + kTileN - 1) / kTileN : 0;
-    it.npad = max(kMinItemIters, (it.ntiles + 3) & ~3);
-    const int kvh = h / (ap->p.nhead_q / ap->p.nhead_k);
-    it.k = (const char*)(ap->p.k + (int64_t)b * ap->p.batch_stride_k + (int64_t)kvh * ap->p.nhead_stride_k);
-    it.v = (const char*)(ap->p.v + (int64_t)b * ap->p.batch_stride_v + (int64_t)kvh * ap->p.nhead_stride_v);
-    return it;
-}
-
-template <bool kCausal>
-__device__ __forceinline__ void fwd_persistent(const Ring& ring, lds_char* qbuf) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l32 = lane & 31;
-    const int hi = lane >> 5;
-
-    // per-lane constants (VGPRs), as the regular form
-    int k_ld_off0, k_ld_off1, v_ld_off0, v_ld_off1;
-    {
-        ArgsPtr ap = args_here();
-        const int ld_row = (kLoadsPerTile * wave) * 8 + (lane >> 3);
-        const int ld_pc = lane & 7;
-        k_ld_off0 = ld_row * ap->p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row)) << 4);
-        k_ld_off1 = (ld_row + 8) * ap->p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row + 8)) << 4);
-        v_ld_off0 = ld_row * ap->p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row)) << 4);
-        v_ld_off1 = (ld_row + 8) * ap->p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row + 8)) << 4);
-    }
-    const int wave_off = (kLoadsPerTile * wave) * 1024;
-    // This wave's Q buffer: its 32 Q rows, swizzled as K rows (the GEMM0 B
-    // operand is read with the K read pattern); also the O staging of the
-    // epilogue and, in wave 0's, the successor mailbox.
-    lds_char* const qw = qbuf + wave * (kRowsPerWave * kRowBytes);
-
-    uint32_t k_rd[4];
-    {
-        const int f = k_swz(l32);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) k_rd[t] = l32 * kRowBytes + (((2 * t + hi) ^ f) << 4);
-    }
-    uint32_t v_rd[2];
-    {
-        const int g = lane >> 4, i16 = lane & 15;
-        const int e = i16 >> 2, c = i16 & 3;
-        const int row = 4 * hi + e;
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-            const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-            v_rd[db] = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
-        }
-    }
-
-    bf16x8 qop[4];
-    f32x16 oacc[2];
-    f32x16 sacc[2][2];
-    bf16x8 pbuf[2][4];
-    Softmax sm{kMaxSeed, 0.0f, 0.0f};
-    Softmax smz{kMaxSeed, 0.0f, 0.0f};  // the previous item's, until its epilogue
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
-
-    const int n_blocks = gridDim.x;
-    // the queue of the XCD this block runs on (any queue is correct; this one
-    // keeps a head's items, hence its K/V, on one XCD): items n_blocks + qsel
-    // + 8k are = xcc (mod 8)
-    int qsel;
-    {
-        int xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        qsel = ((xcc & (kQueues - 1)) - n_blocks) & (kQueues - 1);
-    }
-
-    // The item in progress (number LX, ring view X, per-item constants), its
-    // successor's number LN (known from X's iteration 3 on) and its
-    // predecessor's LZ (whose last GEMM1 and epilogue run in X's iteration 0).
-    int LX = blockIdx.x;
-    int LN = 0;
-    int LZ = 0;
-    ItemKV X;
-    int sk, shift;
-    uint32_t kbytes, vbytes;
-    int k_tile_step, v_tile_step;
-    float scale, scale_v;
-    auto load_item = [&]() {  // X's view and the per-launch constants, reloaded per item
-        ArgsPtr ap = args_here();
-        X = item_kv<kCausal>(ap, LX);
-        sk = ap->p.seqlen_k;
-        shift = sk - ap->p.seqlen_q;
-        kbytes = sk > 0 ? (uint32_t)((int64_t)(sk - 1) * ap->p.stride_k * 2 + kRowBytes) : 0u;
-        vbytes = sk > 0 ? (uint32_t)((int64_t)(sk - 1) * ap->p.stride_v * 2 + kRowBytes) : 0u;
-        k_tile_step = kTileN * ap->p.stride_k * 2;
-        v_tile_step = kTileN * ap->p.stride_v * 2;
-        scale = ap->p.scale;
-        scale_v = in_vgpr(scale);
-    };
-
-    // DMA of X's tile `tile` (K or V) into stage S; `view` may be the
-    // successor's (the tail group)
-    auto issue_k = [&](const ItemKV& view, int tile, auto stage_c) {
-        lds_char* dst = ring.k[decltype(stage_c)::value] + wave_off;
-        const uint32_t t0 = (uint32_t)tile * (uint32_t)k_tile_step;
-        const auto r = make_rsrc(view.k + t0, tile < view.ntiles ? kbytes - t0 : 0u);
-        lds_dma_16(r, dst, k_ld_off0);
-        lds_dma_16(r, dst + 1024, k_ld_off1);
-    };
-    auto issue_v = [&](const ItemKV& view, int tile, auto stage_c) {
-        lds_char* dst = ring.v[decltype(stage_c)::value] + wave_off;
-        const uint32_t t0 = (uint32_t)tile * (uint32_t)v_tile_step;
-        const auto r = make_rsrc(view.v + t0, tile < view.ntiles ? vbytes - t0 : 0u);
-        lds_dma_16(r, dst, v_ld_off0);
-        lds_dma_16(r, dst + 1024, v_ld_off1);
-    };
-    auto issue_q = [&](int L) {  // this wave's 32 Q rows of item L into its Q buffer
-        ArgsPtr ap = args_here();
-        int b, h, mt;
-        item_coords<kCausal>(ap, L, b, h, mt);
-        const int sq = ap->p.seqlen_q, sq_stride = ap->p.stride_q;
-        const uint32_t qbytes = sq > 0 ? (uint32_t)((int64_t)(sq - 1) * sq_stride * 2 + kRowBytes) : 0u;
-        const char* q = (const char*)(ap->p.q + (int64_t)b * ap->p.batch_stride_q + (int64_t)h * ap->p.nhead_stride_q);
-        const uint32_t r0 = (uint32_t)(mt * kTileM) * (uint32_t)(sq_stride * 2);
-        const auto r = make_rsrc(q + r0, qbytes > r0 ? qbytes - r0 : 0u);
-        // load i: rows 8i + lane/8 of the wave's 32; physical chunk lane%8
-        // holds logical chunk (lane%8) ^ k_swz(row) = (lane%8) ^ (lane/8) ^ (i&1)
-        const int row = wave * kRowsPerWave + (lane >> 3);
-        const int base_off = row * sq_stride * 2;
-        const int sw = (lane & 7) ^ (lane >> 3);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            lds_dma_16(r, qw + i * 1024, base_off + i * 8 * sq_stride * 2 + ((sw ^ (i & 1)) << 4));
-    };
-    auto gemm0 = [&](auto ks_c, f32x16* s) {
-        const lds_char* st = ring.k[decltype(ks_c)::value];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x16 acc = {};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) acc = mfma(lds_read_b128(st + k_rd[k] + kb * 32 * kRowBytes), qop[k], acc);
-            s[kb] = acc;
-        }
-    };
-    auto gemm1 = [&](auto vs_c, const bf16x8* pp) {
-        const lds_char* st = ring.v[decltype(vs_c)::value];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int k = 0; k < 2; ++k)
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-                    oacc[db] = mfma(lds_read_vt(st + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[2 * kb + k],
-                                    oacc[db]);
-    };
-    auto mask_tile = [&](int t, f32x16* s) {  // X's tile t
-        const int key0 = t * kTileN;
-        const int wrow0 = X.row0 + wave * kRowsPerWave;
-        const bool need = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
-        if (need) {
-            const int lim = kCausal ? min(sk - 1, wrow0 + l32 + shift) : sk - 1;
-            const int d = lim - (key0 + 4 * hi);
-            const float ninf = in_vgpr(-__builtin_inff());
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
-                    s[kb][r] = c <= d ? s[kb][r] : ninf;
-                }
-        }
-    };
-    auto tile_max = [&](const f32x16* s) {
-        float mp[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) mp[i] = fmaxf(fmaxf(s[i >> 2][4 * (i & 3)], s[i >> 2][4 * (i & 3) + 1]),
-                                                  fmaxf(s[i >> 2][4 * (i & 3) + 2], s[i >> 2][4 * (i & 3) + 3]));
-        const float mx = fmaxf(fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3])),
-                               fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7])));
-        return wave_max_halves(mx);
-    };
-    auto exp_tile = [&](const f32x16* s, bf16x8* pp) {
-        const float neg_ms = -sm.m_ref;
-        float ls[4];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                bf16x8 pk;
-                float acc;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 * k + e], scale_v, neg_ms));
-                    acc = e == 0 ? pv : acc + pv;
-                    pk[e] = (__bf16)pv;
-                }
-                ls[2 * kb + k] = acc;
-                pp[2 * kb + k] = pk;
-            }
-        sm.l_tile = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    };
-    auto softmax = [&](const f32x16* s, bf16x8* pp) {
-        exp_tile(s, pp);
-        asm volatile("" ::"v"(pp[0]), "v"(pp[1]), "v"(pp[2]), "v"(pp[3]), "v"(sm.l_tile));
-    };
-    auto settle = [&](const f32x16* s, bf16x8* pp) {
-        if (__builtin_amdgcn_ballot_w64(!(sm.l_tile <= kGrowSum))) {
-            asm volatile("" ::: "memory");
-            const float m_new = fmaxf(sm.m_ref, tile_max(s) * scale);
-            const float alpha = __builtin_amdgcn_exp2f(sm.m_ref - m_new);
-            sm.m_ref = m_new;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-            sm.l_part *= alpha;
-            exp_tile(s, pp);
-        }
-        sm.l_part += sm.l_tile;
-    };
-    // O = O^T / l and LSE of item L (softmax state `st`), staged through this
-    // wave's Q buffer as the regular form's epilogue stages through a K stage
-    auto epilogue = [&](int L, const Softmax& st) {
-        ArgsPtr ap = args_here();
-        int b, h, mt;
-        item_coords<kCausal>(ap, L, b, h, mt);
-        const int sq = ap->p.seqlen_q, so = ap->p.stride_o;
-        const float l_tot = wave_sum_halves(st.l_part);
-        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        const uint32_t obytes = (uint32_t)((int64_t)(sq - 1) * so * 2 + kRowBytes);
-        const auto ro = make_rsrc(ap->p.o + (int64_t)b * ap->p.batch_stride_o + (int64_t)h * ap->p.nhead_stride_o,
-                                  obytes);
-        const int wrow0 = mt * kTileM + wave * kRowsPerWave;
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                bf16x2 x0, x1;
-                x0[0] = (__bf16)(oacc[db][4 * g4 + 0] * inv);
-                x0[1] = (__bf16)(oacc[db][4 * g4 + 1] * inv);
-                x1[0] = (__bf16)(oacc[db][4 * g4 + 2] * inv);
-                x1[1] = (__bf16)(oacc[db][4 * g4 + 3] * inv);
-                i32x2 w;
-                w[0] = __builtin_bit_cast(int, x0);
-                w[1] = __builtin_bit_cast(int, x1);
-                const int c = 4 * db + g4;
-                *(lds_i32x2*)(qw + l32 * kRowBytes + ((c ^ ((l32 >> 1) & 7)) << 4) + 8 * (hi ^ (l32 & 1))) = w;
-            }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < kRowsPerWave / 8; ++i) {
-            const int r = 8 * i + (lane >> 3), pc = lane & 7;
-            const i32x4 raw = *(const lds_i32x4*)(qw + r * kRowBytes + (pc << 4));
-            const i32x4 v = (r & 1) ? i32x4{raw[2], raw[3], raw[0], raw[1]} : raw;
-            const int c = pc ^ ((r >> 1) & 7);
-            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * so * 2 + c * 16, 0, 0);
-        }
-        const int my_row = wrow0 + l32;
-        float* const lse = ap->p.lse;
-        if (lse != nullptr && hi == 0 && my_row < sq) {
-            const float lse2 = __builtin_log2f(l_tot) + st.m_ref;
-            lse[(int64_t)b * ap->p.nhead_q * sq + (int64_t)h * sq + my_row] = lse2 * 0.69314718055994530942f;
-        }
-        // the staging reads must be done before this buffer takes Q rows again
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    };
-
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    using P2 = std::integral_constant<int, 2>;
-    using P3 = std::integral_constant<int, 3>;
-
-    // one ring iteration t of X (phase J = t % 4): GEMM1(t-1) || GEMM0(t+1)
-    // || softmax(t); its K(t+4) and V(t+2) DMAs come from `kv`/`vv` (X's view,
-    // or the successor's in the tail group, with the tile counted from it)
-    auto iteration = [&](int t, auto phase_c, const ItemKV& kv, int kt, const ItemKV& vv, int vt) {
-        constexpr int J = decltype(phase_c)::value;
-        constexpr int cur = J & 1, nxt = cur ^ 1;
-        vmcnt_wait<4 * kLoadsPerTile>();
-        ring_barrier();
-        issue_k(kv, kt, std::integral_constant<int, J>{});
-        issue_v(vv, vt, std::integral_constant<int, (J + 2) % kRing>{});
-        mask_tile(t, sacc[cur]);
-        gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[nxt]);
-        gemm0(std::integral_constant<int, (J + 1) % kRing>{}, sacc[nxt]);
-        softmax(sacc[cur], pbuf[cur]);
-        IterSchedule<true, true>::apply();
-        settle(sacc[cur], pbuf[cur]);
-    };
-    auto mid = [&](int t, auto phase_c) { iteration(t, phase_c, X, t + kRing, X, t + 2); };
-
-    // iteration 0 of X: X's frame from its first tile's exact max; GEMM1 of
-    // the predecessor's last tile (kPrev), whose epilogue follows
-    int ret = 0;
-    auto first = [&](auto prev_c) {
-        constexpr bool kPrev = decltype(prev_c)::value;
-        vmcnt_wait<4 * kLoadsPerTile>();
-        ring_barrier();
-        if (wave == 0 && lane == 0) {  // X's successor, before the DMAs (the vmcnt waits retire it by iteration 2)
-            ArgsPtr ap = args_here();
-            ret = atomicAdd(ap->queue + qsel * kQueueStride, 1);
-        }
-        issue_k(X, kRing, P0{});
-        issue_v(X, 2, P2{});
-        mask_tile(0, sacc[0]);
-        sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]) * scale);
-        if constexpr (kPrev) gemm1(P3{}, pbuf[1]);
-        gemm0(P1{}, sacc[1]);
-        softmax(sacc[0], pbuf[0]);
-        IterSchedule<kPrev, true>::apply();
-        sm.l_part = sm.l_tile;  // exact frame: nothing to re-frame
-        if constexpr (kPrev) {
-            epilogue(LZ, smz);
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
-        }
-    };
-    // iterations 1-3: the successor handover (npad >= 8: none of these is
-    // among X's last four); iteration 2: wave 0 publishes the successor in
-    // its Q buffer; iteration 3: every wave reads it
-    auto handover = [&]() {
-        mid(1, P1{});
-        {
-            vmcnt_wait<4 * kLoadsPerTile>();  // retires the atomic (issued before iteration 0's DMAs)
-            ring_barrier();
-            issue_k(X, 2 + kRing, P2{});
-            issue_v(X, 2 + 2, P0{});
-            if (wave == 0) {
-                const int k = __builtin_amdgcn_readfirstlane(ret);
-                if (lane == 0) *(__attribute__((address_space(3))) int*)qw = n_blocks + qsel + kQueues * k;
-            }
-            mask_tile(2, sacc[0]);
-            gemm1(P1{}, pbuf[1]);
-            gemm0(P3{}, sacc[1]);
-            softmax(sacc[0], pbuf[0]);
-            IterSchedule<true, true>::apply();
-            settle(sacc[0], pbuf[0]);
-        }
-        {
-            vmcnt_wait<4 * kLoadsPerTile>();
-            ring_barrier();
-            issue_k(X, 3 + kRing, P3{});
-            issue_v(X, 3 + 2, P1{});
-            LN = __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(3))) int*)qbuf);
-            mask_tile(3, sacc[1]);
-            gemm1(P2{}, pbuf[0]);
-            gemm0(P0{}, sacc[0]);
-            softmax(sacc[1], pbuf[1]);
-            IterSchedule<true, true>::apply();
-            settle(sacc[1], pbuf[1]);
-        }
-    };
-    // X's last four iterations: K(t+4) is the successor's tile t+4-npad, V(t+2)
-    // too from npad-2 on; the successor's Q rows come into the Q buffer after
-    // iteration npad-4 and into qop before the last iteration's GEMM0 (its
-    // first tile); a dead successor (none left) loads zero tiles
-    auto tail = [&]() {
-        const int t = X.npad - kRing;
-        const ItemKV N = item_kv<kCausal>(args_here(), LN);
-        const bool has_next = N.ntiles > 0 || LN < args_here()->n_items;
-        iteration(t, P0{}, N, 0, X, t + 2);
-        if (has_next) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the Q buffer's staging and mailbox reads done
-            issue_q(LN);
-        }
-        iteration(t + 1, P1{}, N, 1, X, t + 3);
-        iteration(t + 2, P2{}, N, 2, N, 0);
-        {
-            vmcnt_wait<4 * kLoadsPerTile>();  // also retires the Q DMA (issued before iteration t+1's loads)
-            ring_barrier();
-            issue_k(N, 3, P3{});
-            issue_v(N, 1, P1{});
-            if (has_next) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) qop[k] = lds_read_b128(qw + k_rd[k]);
-            }
-            mask_tile(t + 3, sacc[1]);
-            gemm1(P2{}, pbuf[0]);
-            gemm0(P0{}, sacc[0]);
-            softmax(sacc[1], pbuf[1]);
-            IterSchedule<true, true>::apply();
-            settle(sacc[1], pbuf[1]);
-        }
-        return has_next;
-    };
-
-    load_item();
-    if (X.ntiles > 0 || LX < args_here()->n_items) {
-        // prologue of the block's first item: Q straight into registers, K0 K1
-        // V0 K2 V1 K3 in flight, GEMM0 of tile 0 once Q and K0 landed
-        {
-            ArgsPtr ap = args_here();
-            int b, h, mt;
-            item_coords<kCausal>(ap, LX, b, h, mt);
-            const int sq = ap->p.seqlen_q;
-            const uint32_t qbytes = sq > 0 ? (uint32_t)((int64_t)(sq - 1) * ap->p.stride_q * 2 + kRowBytes) : 0u;
-            const auto rq = make_rsrc(ap->p.q + (int64_t)b * ap->p.batch_stride_q + (int64_t)h * ap->p.nhead_stride_q,
-                                      qbytes);
-            const int qoff = (X.row0 + wave * kRowsPerWave + l32) * ap->p.stride_q * 2 + hi * 16;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
-                qop[t] = __builtin_bit_cast(bf16x8, raw);
-            }
-        }
-        issue_k(X, 0, P0{});
-        issue_k(X, 1, P1{});
-        issue_v(X, 0, P0{});
-        issue_k(X, 2, P2{});
-        issue_v(X, 1, P1{});
-        issue_k(X, 3, P3{});
-        vmcnt_wait<5 * kLoadsPerTile>();
-        ring_barrier();
-        asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
-        gemm0(P0{}, sacc[0]);
-        bool prev = false;
-        while (true) {
-            if (prev)
-                first(std::true_type{});
-            else
-                first(std::false_type{});
-            handover();
-            for (int t = kRing; t < X.npad - kRing; t += kRing) {
-                mid(t, P0{});
-                mid(t + 1, P1{});
-                mid(t + 2, P2{});
-                mid(t + 3, P3{});
-            }
-            if (!tail()) break;
-            LZ = LX;
-            smz = sm;
-            LX = LN;
-            load_item();
-            prev = true;
-        }
-        // drain: the last item's last GEMM1 and its epilogue
-        vmcnt_wait<0>();
-        ring_barrier();
-        gemm1(P3{}, pbuf[1]);
-        epilogue(LX, sm);
-    }
-
-    // the last block to finish leaves the queues at zero for the next launch
-    if (threadIdx.x == 0) {
-        ArgsPtr ap = args_here();
-        int* const queue = ap->queue;
-        if (atomicAdd(queue + kQueues * kQueueStride, 1) == n_blocks - 1) {
-#pragma unroll
-            for (int i = 0; i <= kQueues; ++i) __hip_atomic_store(queue + i * kQueueStride, 0, __ATOMIC_RELAXED,
-                                                                  __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
-// ===========================================================================
 // Short form (this build's own; no counterpart in the reference): the
 // regular grid at four blocks per compute unit (<= 128 VGPRs and 32 KiB of
 // LDS; the regular form fits two), for launches whose M-tiles see few key
@@ -1700,47 +1157,6 @@ FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1_tilemajor(FmhaFwdParams par
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1_tilemajor(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
     fwd_mtile<true, false, kModePair>(params, blockIdx.y, blockIdx.x, gridDim.z - 1 - blockIdx.z, ring);
-}
-
-// ---- persistent entries (this build's own; no counterpart in the
-// reference): one block per resident slot looping over the dense grid's
-// M-tiles; launched only by fmha_fwd_d64_bf16() (their kernarg carries the
-// library's queue counters).  80 KiB of LDS: two blocks per compute unit. ----
-FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_persist_msk0(PersistArgs args) {
-    FMHA_RING(ring, kTileBytes)
-    __shared__ __attribute__((aligned(1024))) char qbuf[kQBufBytes];
-    (void)args;  // read through the kernarg segment pointer
-    fwd_persistent<false>(ring, (lds_char*)qbuf);
-}
-FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_persist_msk1(PersistArgs args) {
-    FMHA_RING(ring, kTileBytes)
-    __shared__ __attribute__((aligned(1024))) char qbuf[kQBufBytes];
-    (void)args;
-    fwd_persistent<true>(ring, (lds_char*)qbuf);
-}
-
-// The persistent form's queue counters: kQueueSlots launch slots, each
-// kQueues queue heads plus a blocks-done counter on their own 128-byte lines.
-// Zero at load; every launch leaves its slot at zero (the last block resets
-// it).  Launches take the slots in turn, so up to kQueueSlots launches of the
-// persistent form may be in flight on one device at once.
-static constexpr int kQueueSlots = FMHA_PERSIST_QUEUE_SLOTS;
-static __device__ __align__(256) int g_persist_queues[kQueueSlots * (kQueues + 1) * kQueueStride];
-
-// Device address of slot `slot` of the current device's counters (the
-// symbol's address is looked up once per device), or null on failure.
-extern "C" int* fmha_persist_queue_slot(unsigned slot) {
-    static std::atomic<int*> base[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    int* b = base[dev].load(std::memory_order_acquire);
-    if (b == nullptr) {
-        void* ptr = nullptr;
-        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_persist_queues)) != hipSuccess || ptr == nullptr) return nullptr;
-        b = (int*)ptr;
-        base[dev].store(b, std::memory_order_release);
-    }
-    return b + (size_t)(slot % kQueueSlots) * (kQueues + 1) * kQueueStride;
 }
 
 // ---- balanced causal entries (this build's own; no counterpart in the

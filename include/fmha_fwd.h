@@ -41,7 +41,9 @@
  *  (16-byte rows); seqlen_* >= 0; nhead_k > 0; nhead_q % nhead_k == 0; both or
  *  neither seqstart pointer set; every in-tensor offset of one (batch, head)
  *  fits in 31 bits; the grid fits (ceil(seqlen_q / kM0) <= 65535 and
- *  batch <= 65535).  Violations return hipErrorInvalidValue and launch nothing.
+ *  batch <= 65535); scale finite and > 0 (the running row maximum assumes
+ *  that a larger score is a larger weight).  Violations return
+ *  hipErrorInvalidValue and launch nothing.
  */
 #ifndef FMHA_FWD_H_
 #define FMHA_FWD_H_
@@ -129,13 +131,6 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *   FMHA_VARIANT_SPLITKV  the splitkv entries (FMHA_SPLIT_KBLOCK threads)
  *   FMHA_VARIANT_PAIR     the pair entries: one FMHA_SPLIT_KBLOCK-thread block
  *                         per two adjacent M-tiles of a (batch, head)
- *   FMHA_VARIANT_PERSISTENT  dense (not varlen) only: one kBlockSize-thread
- *                         block per resident slot (two per compute unit),
- *                         each looping over M-tiles taken from per-XCD queues
- *                         with its K/V pipeline running on from one M-tile
- *                         into the next; its queue counters live in the
- *                         library (device memory it owns, no allocation per
- *                         call; at most 64 such launches in flight per device)
  *   FMHA_VARIANT_SHORT    the short entries: the regular grid at four blocks
  *                         per compute unit, K and V streamed through
  *                         two-stage LDS rings, any number of keys
@@ -149,7 +144,7 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
 #define FMHA_VARIANT_PAIR 3
-#define FMHA_VARIANT_PERSISTENT 4
+/* 4: retired (returns hipErrorInvalidValue) */
 #define FMHA_VARIANT_BALANCED 5 /* fmha_fwd_d64_bf16_ws only: it needs a workspace */
 #define FMHA_VARIANT_SHORT 6
 #define FMHA_VARIANT_BALANCED_PAIR 7 /* fmha_fwd_d64_bf16_ws only: the balanced form over M-tile pairs */
@@ -227,7 +222,8 @@ hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int c
 /* The form FMHA_VARIANT_AUTO resolves to for these arguments on a device with
  * `compute_units` compute units (0 = the current device's count), without
  * launching (this build's own; no counterpart in the reference).  Returns
- * FMHA_VARIANT_REGULAR, _SPLITKV or _PAIR, or -1 for rejected arguments. */
+ * FMHA_VARIANT_REGULAR, _SPLITKV, _PAIR or _SHORT, or -1 for rejected
+ * arguments. */
 int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* params, int batch, int causal, int compute_units);
 
 /* 1 when a launch with these arguments (without FMHA_VARIANT_REFERENCE_ORDER)

@@ -34,8 +34,8 @@ def asm(tmp_path_factory):
 
 
 def _functions(src):
-    """Body of every function symbol (data symbols, such as the persistent
-    form's queue counters, have labels too but no .Lfunc_end)."""
+    """Body of every function symbol (data symbols have labels too but no
+    .Lfunc_end)."""
     funcs = {}
     for name in re.findall(r"^\s*\.type\s+(_Z[^,\s]+),@function", src, re.M):
         m = re.search(r"^" + re.escape(name) + r":", src, re.M)
@@ -48,8 +48,6 @@ def test_every_entry_compiled(asm):
     names = _functions(asm)
     for e in _ENTRIES:
         assert any(e + "13FmhaFwdParams" in n for n in names), e
-    for m in (0, 1):
-        assert any(f"fmha_fwd_d64_bf16_persist_msk{m}" in n for n in names), m
     for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_pair_msk1",
               "fmha_fwd_d64_bf16_balanced_merge"):
         assert any(e in n for n in names), e

@@ -18,8 +18,8 @@ an instruction writes it; an implicit-def is reported where the register may
 still hold the id on some path reaching it (the faulting build's case: its
 implicit-def sat on the path where the register was never written).  An
 implicit-def after the register was overwritten on every path concerns an
-ordinary value (the persistent entries copy blockIdx.x out in their first
-instruction and reuse the register).
+ordinary value (an entry that copies an id out in its first instruction may
+reuse the register).
 """
 import os
 import re

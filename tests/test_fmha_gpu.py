@@ -34,12 +34,10 @@ def _report(res):
     return res
 
 
-# every kernel form behind the launcher: the reference-named entries, the
-# split-KV entries, the pair entries and the persistent entries (the
-# automatic choice is one of them); the persistent form takes dense problems
-# only (the launcher rejects varlen for it)
-FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR,
-         "persistent": fmha.VARIANT_PERSISTENT}
+# every kernel form behind the launcher without a workspace: the
+# reference-named entries, the split-KV entries and the pair entries (the
+# automatic choice is one of them or the short form)
+FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR}
 # the balanced form (causal dense, through the workspace entry) runs on the
 # matrices of reference cases and benchmark configurations
 MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, balanced_pair=fmha.VARIANT_BALANCED_PAIR,
@@ -47,8 +45,6 @@ MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, balanced_pair=fmha.VA
 
 
 def _dense_only(form, prob):
-    if form == "persistent" and prob.varlen:
-        pytest.skip("the persistent form takes dense problems only")
     if form.startswith("balanced") and (prob.varlen or not prob.causal):
         pytest.skip("the balanced forms take causal dense problems only")
 
@@ -154,8 +150,6 @@ def test_gqa_equals_replicated_mha_bitwise(form):
 
 @pytest.mark.parametrize("form", list(FORMS))
 def test_varlen_equals_per_sequence_dense_bitwise(form):
-    if form == "persistent":
-        pytest.skip("the persistent form takes dense problems only")
     seqs = (1, 77, 128, 300, 64, 513)
     pv = Problem(batch=0, nhead_q=4, nhead_k=2, seqlen_q=0, causal=True, lse=True, varlen_seqs=seqs)
     q, k, v = make_inputs(pv, "normal", 5)
@@ -227,8 +221,6 @@ def test_masked_and_foreign_keys_contribute_nothing(form):
     wrongly included key would get a sizeable weight; V = 16384.0); the
     row's output bits must not change.  (1) the other sequences of a packed varlen batch, (2) the
     causally masked future key."""
-    if form == "persistent":
-        pytest.skip("the persistent form takes dense problems only")
     seqs = (190, 64, 333)
     T = sum(seqs)
     s0 = seqs[0]
@@ -447,20 +439,20 @@ def test_padded_strides_match_dense(form):
     assert np.array_equal(dl.cpu().numpy(), l_dense)
 
 
-def test_persistent_rejects_varlen():
-    """The persistent form is dense only: a varlen launch asking for it is
-    refused before anything runs."""
+def test_retired_variant_rejected():
+    """Variant value 4 (a queue-based persistent form, removed) is refused
+    before anything runs, as any unknown variant."""
     import torch
 
     from harness import build_params
 
-    p = Problem(batch=0, nhead_q=2, seqlen_q=0, varlen_seqs=(100, 200))
+    p = Problem(batch=1, nhead_q=2, seqlen_q=100)
     nq, nk, nlse = p.sizes()
     t = [torch.zeros(n, dtype=torch.int16, device="cuda:0") for n in (nq, nk, nk, nq)]
-    seq = torch.from_numpy(p.seqstart()).to("cuda:0")
-    prm = build_params(p, *t, None, seq)
-    with pytest.raises(fmha.FmhaError):
-        fmha.fmha_fwd_d64_bf16(prm, p.batch, 0, None, fmha.VARIANT_PERSISTENT)
+    prm = build_params(p, *t, None, None)
+    for v in (4, 8, -1):
+        with pytest.raises(fmha.FmhaError):
+            fmha.fmha_fwd_d64_bf16(prm, p.batch, 0, None, v)
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -545,64 +537,3 @@ def test_short_equals_regular_on_long_rows(causal, sq, sk):
     empty = np.isinf(l_r)  # causal rows with no visible key: LSE -inf in both, O 0
     assert np.array_equal(l_s[empty], l_r[empty]) and np.all(a.reshape(-1, 64)[empty] == 0)
     assert np.abs(l_s[~empty] - l_r[~empty]).max() <= 1e-4
-
-
-@pytest.mark.parametrize("causal", [False, True])
-def test_persistent_queue_state_across_launches(causal):
-    """The persistent form's queue counters are left at zero by every launch:
-    launches of different shapes in a row (many items, fewer items than
-    resident blocks, one item, again many) each give the regular form's bits.
-    A counter left behind would make a later launch skip items (rows left at
-    the sentinel) or run the wrong ones."""
-    shapes = [(4, 16, 16, 2048, 2048), (1, 3, 1, 300, 517), (1, 1, 1, 64, 64), (2, 8, 2, 1500, 1000),
-              (3, 16, 8, 4100, 4100)]
-    for b, h, hk, sq, sk in shapes:
-        p = Problem(batch=b, nhead_q=h, nhead_k=hk, seqlen_q=sq, seqlen_k=sk, causal=causal, lse=True)
-        q, k, v = make_inputs(p, "normal", sq + sk)
-        o_p, l_p = run_kernel(p, q, k, v, variant=fmha.VARIANT_PERSISTENT)
-        o_r, l_r = run_kernel(p, q, k, v, variant=fmha.VARIANT_REGULAR)
-        print("persistent vs regular", (b, h, hk, sq, sk), flush=True)
-        assert np.array_equal(o_p, o_r), (b, h, sq, sk)
-        assert np.array_equal(l_p, l_r), (b, h, sq, sk)
-
-
-def test_persistent_graph_replays_and_concurrent_streams():
-    """Graph capture: every replay (eager work between them) reproduces the
-    eager bits, so the counters a launch leaves behind are what the next
-    replay needs.  Concurrent launches on two streams take different counter
-    slots and give each its own bits."""
-    import torch
-
-    pa = Problem(batch=2, nhead_q=8, nhead_k=4, seqlen_q=2000, seqlen_k=2000, causal=True, lse=True)
-    pb = Problem(batch=4, nhead_q=16, seqlen_q=1024, lse=True)
-    ka, oa, la, prma = _device_problem(pa, 41)
-    kb, ob, lb, prmb = _device_problem(pb, 42)
-    P = fmha.VARIANT_PERSISTENT
-    fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, None, fmha.VARIANT_REGULAR)
-    fmha.fmha_fwd_d64_bf16(prmb, pb.batch, 0, None, fmha.VARIANT_REGULAR)
-    torch.cuda.synchronize()
-    ref_a, ref_la, ref_b, ref_lb = oa.clone(), la.clone(), ob.clone(), lb.clone()
-    s = torch.cuda.Stream()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, torch.cuda.current_stream().cuda_stream, P)
-    noise = torch.randn(1 << 20, device="cuda:0")
-    for i in range(4):
-        oa.zero_()
-        la.zero_()
-        noise.mul_(1.0001)
-        torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(oa, ref_a) and torch.equal(la, ref_la), i
-    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
-    for _ in range(3):
-        oa.zero_()
-        ob.zero_()
-        torch.cuda.synchronize()
-        for _ in range(4):
-            fmha.fmha_fwd_d64_bf16(prma, pa.batch, 1, sa.cuda_stream, P)
-            fmha.fmha_fwd_d64_bf16(prmb, pb.batch, 0, sb.cuda_stream, P)
-        torch.cuda.synchronize()
-        assert torch.equal(oa, ref_a) and torch.equal(la, ref_la)
-        assert torch.equal(ob, ref_b) and torch.equal(lb, ref_lb)
