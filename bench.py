@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 D64 BF16 FMHA forward (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--cpu-all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 Metric: forward TFLOP/s (repo FLOP convention 4*B*H*Sq*Sk*D, x0.5 when
 causal; reference src/bench_fmha_fwd.cpp:225-226) and its fraction of the
@@ -22,13 +22,13 @@ rocprofv3 run of the same kernel (profiles/), its HBM traffic, MFMA busy
 fraction and clock.
 
 The CPU baseline is the reference's own CPU path, cpu_ref_verify, compiled
-from its sources into oracle/_ref/ref_verify and timed over the whole
-workload of both metric configurations on this host ("kind": "reference");
-where that harness was not built, the faithful C restatement (oracle/) on a
-bounded row sample ("kind": "port").  ``--cpu-all`` adds cfg1 and cfg4 (the
-reference, whole workloads) and cfg5 (the port on a row sample: the whole
-workload takes its loop minutes on one thread).  Only this leg touches
-oracle/.
+from its sources into oracle/_ref/ref_verify and timed on this host for all
+five benchmark configurations ("kind": "reference"): cfg1, cfg2 and cfg4 over
+the whole workload, cfg3 over 4 of its 16 heads and cfg5 over the last 4000
+of its 40000 query rows of one head, each scaled to its workload (the whole
+of cfg3 and cfg5 would take its loop minutes on one thread).  Where that
+harness was not built, the faithful C restatement (oracle/) on a bounded row
+sample ("kind": "port").  Only this leg touches oracle/.
 """
 import argparse
 import json
@@ -219,7 +219,7 @@ def _host_threads():
     return nproc, omp, threads
 
 
-def cpu_baseline_reference(prob, heads=None):
+def cpu_baseline_reference(prob, heads=None, rows=None):
     """The reference's own CPU path, cpu_ref_verify (src/runner/cpu_ref.cpp:14-311,
     compiled from its sources into oracle/_ref/ref_verify), timed by the
     harness around that one call.  Its loop nest (cpu_ref.cpp:73-84) is
@@ -229,14 +229,18 @@ def cpu_baseline_reference(prob, heads=None):
     sequence) and scale the time to all of them; used where the whole
     workload would take minutes and the sample keeps the loop's parallelism
     (B*H units handed out 16 at a time: both fit one chunk, one thread).
-    None if not built."""
+    ``rows``: run only the last ``rows`` query rows against all of the keys
+    (seqlen_q = rows, seqlen_k unchanged: bottom-right alignment keeps each
+    sampled row's mask) and scale by seqlen_q / rows; every row costs the
+    loop the same seqlen_k dot products both ways.  None if not built."""
     import subprocess
 
     if not os.path.exists(REF_VERIFY):
         return None
     nh = heads or prob.nhead_q
-    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(nh), "-s", str(prob.seqlen_q), "--seed", "42",
-           "--mask", str(int(prob.causal)), "--lse", str(int(prob.lse))]
+    nrows = rows or prob.seqlen_q
+    cmd = [REF_VERIFY, "-b", str(prob.batch), "-h", str(nh), "-s", str(nrows), "--kv-seq", str(prob.seqlen_k),
+           "--seed", "42", "--mask", str(int(prob.causal)), "--lse", str(int(prob.lse))]
     if prob.varlen:
         cmd += ["--varlen-seqs", ",".join(str(x) for x in prob.varlen_seqs)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
@@ -253,14 +257,24 @@ def cpu_baseline_reference(prob, heads=None):
     chunks = -(-units // 16)
     if heads:
         assert -(-(prob.batch * nh) // 16) == chunks == 1, "a head sample must keep the loop's parallelism"
-    t = t_run * prob.nhead_q / nh
+    t = t_run * (prob.nhead_q / nh) * (prob.seqlen_q / nrows)
     lse = f", LSE |d| max {res[0]['lse_max_abs']:.2e}" if prob.lse else ""
     seqs = f"varlen {'/'.join(str(x) for x in prob.varlen_seqs)} H{prob.nhead_q}" if prob.varlen else \
         f"B{prob.batch}H{prob.nhead_q}S{prob.seqlen_q}"
     shape = f"{seqs}{' causal' if prob.causal else ''}{' +LSE' if prob.lse else ''}"
-    what = (f"over {nh} of the {prob.nhead_q} heads of the {shape} workload ({t_run:.2f} s, scaled x{prob.nhead_q}/{nh}"
-            f" to {t:.2f} s: one thread computes every head either way, the B*H units all fitting one chunk of 16)"
-            if heads else f"over the full {shape} workload, {t:.2f} s")
+    if rows:
+        what = (f"over the last {nrows} of the {prob.seqlen_q} query rows (against all {prob.seqlen_k} keys) of "
+                f"{nh} of the {prob.nhead_q} heads of the {shape} workload ({t_run:.2f} s, scaled "
+                f"x{prob.seqlen_q}/{nrows} x{prob.nhead_q}/{nh} to {t:.2f} s: the loop computes every key's score "
+                f"for every row, and one thread computes every head either way; the sampled rows see 90-100 % of "
+                f"their keys against half on average, and only visible keys take expf, so the rate per row is "
+                f"if anything understated)")
+    elif heads:
+        what = (f"over {nh} of the {prob.nhead_q} heads of the {shape} workload ({t_run:.2f} s, scaled "
+                f"x{prob.nhead_q}/{nh} to {t:.2f} s: one thread computes every head either way, the B*H units "
+                f"all fitting one chunk of 16)")
+    else:
+        what = f"over the full {shape} workload, {t:.2f} s"
     out = {
         "value": prob.flops() / t / 1e12,
         "unit": "TFLOP/s",
@@ -320,32 +334,35 @@ def cpu_baseline(prob, host, budget_s=10.0, nthreads=None):
     }
 
 
+# Query rows of cfg5 the reference's CPU loop is timed on (about 12 s on one
+# thread; the whole workload would take it about four minutes).
+CFG5_CPU_ROWS = 4000
+
+
 def cpu_baseline_others():
-    """The CPU baseline on the other benchmark configurations (``--cpu-all``):
-    cfg1 and cfg4 by the reference's own cpu_ref_verify over the whole
-    workload (cfg4: eight sequences x 16 heads, 128 (sequence, head) units in
-    8 chunks of 16, so 8 threads have work); cfg5 (B1 H2 S40000, both units in
-    one chunk: one thread, about 20 minutes in full) by the C port on a row
-    sample, on one thread as the reference's loop would run it."""
+    """The CPU baseline on cfg1, cfg4 and cfg5 (the reference's cpu_ref_verify
+    throughout): cfg1 and cfg4 over the whole workload (cfg4: eight sequences x
+    16 heads, 128 (sequence, head) units in 8 chunks of 16, so 8 threads have
+    work); cfg5 (B1 H2 S40000, both units in one chunk: one thread) over the
+    last CFG5_CPU_ROWS query rows of one head, scaled to the workload.  Where
+    the reference harness is not built, the faithful C port on a row sample."""
     from fmha_native_amd.problem import baseline_problems
 
     keys = ("value", "value_exact_flops", "unit", "cores", "kind", "seconds", "effective_parallelism", "sample")
     out = {}
     probs = baseline_problems()
-    for name in ("cfg1", "cfg4"):
+    for name in ("cfg1", "cfg4", "cfg5"):
         print(f"bench.py: CPU baseline {name}", file=sys.stderr, flush=True)
-        c = cpu_baseline_reference(probs[name][0])
-        if c is not None:
-            out[name] = {k: c[k] for k in keys if k in c}
-    import fmha_native_amd as fmha
+        prob, mult = probs[name]
+        c = cpu_baseline_reference(prob, heads=1, rows=CFG5_CPU_ROWS) if name == "cfg5" else \
+            cpu_baseline_reference(prob)
+        if c is None:
+            import fmha_native_amd as fmha
 
-    print("bench.py: CPU baseline cfg5", file=sys.stderr, flush=True)
-    prob5, mult5 = probs["cfg5"]
-    nq, nk, _ = prob5.sizes()
-    host = (fmha.fill_normal(42, nq, mult5), fmha.fill_normal(43, nk, mult5), fmha.fill_normal(44, nk, mult5))
-    c5 = cpu_baseline(prob5, host, budget_s=20.0, nthreads=1)
-    c5["effective_parallelism"] = 1
-    out["cfg5"] = {k: c5[k] for k in keys if k in c5}
+            nq, nk, _ = prob.sizes()
+            host = (fmha.fill_normal(42, nq, mult), fmha.fill_normal(43, nk, mult), fmha.fill_normal(44, nk, mult))
+            c = cpu_baseline(prob, host, budget_s=10.0, nthreads=None if prob.varlen else 1)
+        out[name] = {k: c[k] for k in keys if k in c}
     return out
 
 
@@ -403,8 +420,6 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-all", action="store_true",
-                    help="also time the CPU baseline on cfg1, cfg4 and cfg5 (about a minute more of host time)")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
     ap.add_argument("--only", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
                     help="time one workload only (profiling runs)")
@@ -475,8 +490,7 @@ def main():
         c3 = cpu_baseline_reference(cfg3, heads=4) or cpu_baseline(cfg3, r3["host"])
         cpu["cfg3"] = {k: c3[k] for k in ("value", "unit", "cores", "kind", "seconds", "effective_parallelism",
                                           "sample") if k in c3}
-        if args.cpu_all:
-            cpu.update(cpu_baseline_others())
+        cpu.update(cpu_baseline_others())
 
     achieved = r2["tflops"]
     line = {

@@ -28,7 +28,7 @@ __all__ = [
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
     "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
-    "VARIANT_REFERENCE_ORDER", "VARIANTS",
+    "VARIANT_REFERENCE_ORDER", "VARIANT_TILE_MAJOR_ORDER", "VARIANT_SEQUENCE_ORDER", "VARIANTS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -125,6 +125,10 @@ VARIANT_BALANCED_PAIR = 7  # the balanced form over M-tile pairs (a workspace, l
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
+# flags: tile-major entries / the level order of causal varlen launches, and
+# the sequence order of causal varlen launches (longest sequence first)
+VARIANT_TILE_MAJOR_ORDER = 32
+VARIANT_SEQUENCE_ORDER = 64
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
             "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
             "balanced_pair": VARIANT_BALANCED_PAIR}
@@ -204,8 +208,11 @@ def pick_variant(params, batch, causal, compute_units=0):
 
 
 def tile_major(params, batch, causal):
-    """1 when the launch runs a tile-major causal entry (every batch's heaviest
-    M-tiles first), 0 for the reference's batch-after-batch order, -1 for
+    """Block order of the automatic launch: 1 for a tile-major causal entry
+    (every batch's heaviest M-tiles first) or the level order of a compact
+    causal varlen entry (the live M-tiles of all sequences, highest M-tile
+    index first), 2 for the sequence order of a compact varlen entry (longest
+    sequence first), 0 for the reference's batch-after-batch order, -1 for
     rejected arguments.  Host only."""
     return load_library().fmha_fwd_d64_bf16_tile_major(ctypes.byref(params), int(batch), int(causal))
 

@@ -13,7 +13,7 @@
 //   --variant auto|regular|splitkv|pair|balanced|balanced_pair|short   kernel form (default: the launcher's choice)
 //   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws, allocated before timing), so the
 //                    automatic choice may be the balanced causal form (default 1); --variant balanced needs it
-//   --order auto|reference   causal block order (reference: batch after batch)
+//   --order auto|reference|tilemajor|sequence   causal block order (reference: batch after batch)
 // It launches through the C-ABI launcher and reports its error code instead
 // of exiting silently on a bad launch.
 
@@ -46,7 +46,7 @@ struct Config {
     unsigned seed = 42;
     std::string dist = "ref";
     int variant = FMHA_VARIANT_AUTO;
-    bool reference_order = false;
+    int order_flag = 0;  // one of the FMHA_VARIANT_*_ORDER flags, or 0
     bool workspace = true;
     float scale_inputs = 1.0f;
     std::vector<int> varlen_seqs;
@@ -70,7 +70,7 @@ static void usage(const char* prog) {
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
            "  --variant V      auto|regular|splitkv|pair|balanced|balanced_pair|short form [auto]\n"
            "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [1]\n"
-           "  --order O        auto|reference causal block order [auto]\n",
+           "  --order O        auto|reference|tilemajor|sequence causal block order [auto]\n",
            prog);
 }
 
@@ -134,9 +134,11 @@ static Config parse(int argc, char** argv) {
                 }
                 break;
             case 8:
-                if (!strcmp(optarg, "auto")) c.reference_order = false;
-                else if (!strcmp(optarg, "reference")) c.reference_order = true;
-                else { fprintf(stderr, "Error: --order must be auto or reference\n"); exit(1); }
+                if (!strcmp(optarg, "auto")) c.order_flag = 0;
+                else if (!strcmp(optarg, "reference")) c.order_flag = FMHA_VARIANT_REFERENCE_ORDER;
+                else if (!strcmp(optarg, "tilemajor")) c.order_flag = FMHA_VARIANT_TILE_MAJOR_ORDER;
+                else if (!strcmp(optarg, "sequence")) c.order_flag = FMHA_VARIANT_SEQUENCE_ORDER;
+                else { fprintf(stderr, "Error: --order must be auto, reference, tilemajor or sequence\n"); exit(1); }
                 break;
             case 9: c.workspace = atoi(optarg) != 0; break;
             case 0: usage(argv[0]); exit(0);
@@ -226,7 +228,7 @@ int main(int argc, char** argv) {
         p.batch_stride_k = p.batch_stride_v = c.kv_heads * c.kv_seq_len * D;
     }
 
-    const int variant = c.variant | (c.reference_order ? FMHA_VARIANT_REFERENCE_ORDER : 0);
+    const int variant = c.variant | c.order_flag;
     void* dws = nullptr;
     int64_t ws_bytes = 0;
     const bool use_ws = c.workspace || c.variant == FMHA_VARIANT_BALANCED || c.variant == FMHA_VARIANT_BALANCED_PAIR;

@@ -147,6 +147,44 @@ bool use_tilemajor(const FmhaFwdParams* p, int batch, int causal) {
     return p->seqlen_k == 0 || (rows <= limit && rows * p->seqlen_k <= limit);
 }
 
+// Block order of causal launches.  Dense batches: the reference's (batch
+// after batch) or the tile-major entries (use_tilemajor).  Varlen launches of
+// at most 64 sequences in the regular form: the reference's order (sequence
+// after sequence in the caller's order, the blocks past each short sequence's
+// end dispatched between live ones) or one of the compact entries on the same
+// grid, whose blocks take the live (sequence, M-tile) items in the level
+// order (highest M-tile index first across all sequences) or the sequence
+// order (longest sequence first, each heaviest M-tile first), the grid's
+// ranks past the live items last.
+enum Order : int { kOrderAuto = 0, kOrderReference = 1, kOrderTileMajor = 2, kOrderSequence = 3 };
+constexpr int kOrderFlags = FMHA_VARIANT_REFERENCE_ORDER | FMHA_VARIANT_TILE_MAJOR_ORDER | FMHA_VARIANT_SEQUENCE_ORDER;
+// the order a variant's flags ask for; -1 for more than one
+int order_of(int variant) {
+    const int f = variant & kOrderFlags;
+    return f == 0                               ? kOrderAuto
+           : f == FMHA_VARIANT_REFERENCE_ORDER  ? kOrderReference
+           : f == FMHA_VARIANT_TILE_MAJOR_ORDER ? kOrderTileMajor
+           : f == FMHA_VARIANT_SEQUENCE_ORDER   ? kOrderSequence
+                                                : -1;
+}
+constexpr int kCompactMaxSeqs = 64;
+bool compact_applies(const FmhaFwdParams* p, int batch, int causal) {
+    return causal && p->seqstart_q != nullptr && batch >= 1 && batch <= kCompactMaxSeqs;
+}
+// The varlen order of a regular-form causal launch: kOrderReference,
+// kOrderTileMajor (level order) or kOrderSequence.
+int varlen_order(const FmhaFwdParams* p, int batch, int causal, int order) {
+    if (!compact_applies(p, batch, causal) || order == kOrderReference) return kOrderReference;
+    if (order != kOrderAuto) return order;
+    return kOrderTileMajor;
+}
+// Dense causal batches on the tile-major entries?
+bool dense_tile_major(const FmhaFwdParams* p, int batch, int causal, int order) {
+    if (order == kOrderReference || order == kOrderSequence) return false;
+    if (order == kOrderTileMajor) return causal && batch >= 2 && p->seqstart_q == nullptr;
+    return use_tilemajor(p, batch, causal);
+}
+
 // Keys up to which the automatic choice takes the short form: on every grid
 // of two blocks' worth of query rows per compute unit, and causal on grids of
 // eight.
@@ -369,7 +407,8 @@ extern "C" int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* p, int batch
 
 extern "C" int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* p, int batch, int causal, int variant) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
-    const int mode = plan_mode(variant & ~FMHA_VARIANT_REFERENCE_ORDER);
+    if (order_of(variant) < 0) return -1;
+    const int mode = plan_mode(variant & ~kOrderFlags);
     if (mode < 0) return 0;
     int64_t bytes = 0;
     if (!balanced_plan(p, batch, causal, device_cus(), mode, nullptr, &bytes)) return 0;
@@ -380,7 +419,8 @@ extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, in
                                            void* workspace, int64_t workspace_bytes, hipStream_t stream) {
     const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
     if (chk != hipSuccess) return chk;
-    const int mode = plan_mode(variant & ~FMHA_VARIANT_REFERENCE_ORDER);
+    if (order_of(variant) < 0) return hipErrorInvalidValue;
+    const int mode = plan_mode(variant & ~kOrderFlags);
     if (mode < 0) return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
     if (workspace_bytes < 0 || (workspace == nullptr && workspace_bytes != 0) ||
         (reinterpret_cast<uintptr_t>(workspace) & 255u))
@@ -414,16 +454,22 @@ extern "C" int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* p, int batch,
 
 extern "C" int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* p, int batch, int causal) {
     if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess) return -1;
-    if (p->seqlen_q == 0) return 0;  // nothing is launched
-    return use_tilemajor(p, batch, causal) ? 1 : 0;
+    if (p->seqlen_q == 0 || batch == 0) return 0;  // nothing is launched
+    if (dense_tile_major(p, batch, causal, kOrderAuto)) return 1;
+    // varlen: the compact orders, which only the regular form has
+    if (pick_form(p, batch, causal, device_cus()) != FMHA_VARIANT_REGULAR) return 0;
+    const int o = varlen_order(p, batch, causal, kOrderAuto);
+    return o == kOrderTileMajor ? 1 : o == kOrderSequence ? 2 : 0;
 }
 
 extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batch, int causal, int variant,
                                                 hipStream_t stream) {
     const hipError_t chk = fmha_fwd_d64_bf16_check(p, batch, causal);
     if (chk != hipSuccess) return chk;
-    const bool tile_major = (variant & FMHA_VARIANT_REFERENCE_ORDER) == 0 && use_tilemajor(p, batch, causal);
-    variant &= ~FMHA_VARIANT_REFERENCE_ORDER;
+    const int order = order_of(variant);
+    if (order < 0) return hipErrorInvalidValue;  // more than one order flag
+    const bool tile_major = dense_tile_major(p, batch, causal, order);
+    variant &= ~kOrderFlags;
     // the balanced forms need fmha_fwd_d64_bf16_ws; 4 is a retired value
     if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_BALANCED ||
         variant == 4)
@@ -487,7 +533,16 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     const dim3 block(kBlockSize);
     if (varlen) {
         if (causal)
-            hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk1_varlen, grid, block, 0, stream, *p);
+            switch (varlen_order(p, batch, causal, order)) {
+                case kOrderTileMajor:
+                    hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk1_varlen_tilemajor, grid, block, 0, stream, *p);
+                    break;
+                case kOrderSequence:
+                    hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk1_varlen_seqmajor, grid, block, 0, stream, *p);
+                    break;
+                default:
+                    hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk1_varlen, grid, block, 0, stream, *p);
+            }
         else
             hipLaunchKernelGGL(fmha_fwd_d64_bf16_msk0_varlen, grid, block, 0, stream, *p);
     } else {

@@ -1061,6 +1061,96 @@ __device__ __forceinline__ void fwd_short(const FmhaFwdParams& p, int b, int h, 
     }
 }
 
+// ===========================================================================
+// Compact causal varlen orders (this build's own; no counterpart in the
+// reference).  The reference's varlen grid (nhead_q, M-tiles of the longest
+// sequence, sequences) runs the sequences one after another in the caller's
+// order, each heaviest M-tile first (kernel.cpp:91-99): the blocks past a
+// short sequence's end are dispatched between live ones, and a long last
+// sequence's heavy M-tiles start last.  On the same grid, block (h, y, z)
+// here takes the item of rank r = z * gridDim.y + y (its place in the
+// dispatch order) in a list of the live (sequence, M-tile) items; the ranks
+// past the live items, dispatched last, exit at once.  Two lists:
+//  * level order: by M-tile index, highest first, then by sequence, so every
+//    sequence's heaviest M-tiles start before any lighter one (a causal
+//    M-tile's key tiles grow with its index);
+//  * sequence order: sequence after sequence, the sequences longest first
+//    (ties: caller's order), each heaviest M-tile first, so a sequence's
+//    M-tiles, which re-read its K/V, still run close together in time.
+// Each wave finds its item from the sequence lengths alone: lane s < batch
+// holds n_s, the M-tiles of sequence s (at most gridDim.y, as the regular
+// grid computes).  Requires batch <= 64 (one lane per sequence); the results
+// are wave-uniform.
+// ===========================================================================
+constexpr int kCompactMaxSeqs = 64;
+
+// This lane's sequence's M-tiles (0 past the last sequence).
+__device__ __forceinline__ int compact_ntiles(const FmhaFwdParams& p) {
+    const int lane = threadIdx.x & 63;
+    if (lane >= (int)gridDim.z) return 0;  // gridDim.z <= kCompactMaxSeqs (checked by the launcher)
+    const int len = p.seqstart_q[lane + 1] - p.seqstart_q[lane];
+    return min((len + kTileM - 1) / kTileM, (int)gridDim.y);
+}
+
+// Level order.  The items at level m or above number
+// C(m) = sum_s max(0, n_s - m); the item of rank r sits at the highest level m
+// with C(m) > r, at index r - C(m + 1) among the sequences with n_s > m.  The
+// lanes evaluate C at up to 64 candidate levels at once (the n_s taken from
+// their lanes one by one), narrowing [0, gridDim.y) by 64x per round: one
+// round up to 64 M-tiles per sequence, two up to 4096, three beyond.
+__device__ __forceinline__ bool level_item(const FmhaFwdParams& p, int rank, int& b_out, int& mt_out) {
+    const int lane = threadIdx.x & 63;
+    const int nseq = gridDim.z;
+    const int n = compact_ntiles(p);
+    // [lo, hi): the level holding `rank`; invariant C(lo) > rank (checked
+    // first at lo = 0: otherwise the rank is past the live items)
+    int lo = 0, hi = gridDim.y, c_next = 0;
+    for (;;) {
+        const int step = (hi - lo + 63) >> 6;
+        const int m = lo + lane * step;  // this lane's candidate level (>= hi: none)
+        int c = 0, c1 = 0;               // C(m), C(m + 1)
+        for (int s = 0; s < nseq; ++s) {
+            const int ns = __builtin_amdgcn_readlane(n, s);
+            c += max(0, ns - m);
+            c1 += max(0, ns - m - 1);
+        }
+        const uint64_t above = __builtin_amdgcn_ballot_w64(m < hi && c > rank);
+        if (above == 0) return false;  // only at lo = 0: C(0) <= rank, a dead rank
+        const int top = 63 - __builtin_clzll(above);  // C falls with m: the set lanes are a prefix
+        lo = lo + top * step;
+        c_next = __builtin_amdgcn_readlane(c1, top);
+        if (step == 1) break;
+        hi = min(hi, lo + step);
+    }
+    const int r = rank - c_next;  // index among the sequences with n_s > lo
+    const uint64_t live = __builtin_amdgcn_ballot_w64(n > lo);
+    const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(live >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)live, 0));
+    const uint64_t mine = __builtin_amdgcn_ballot_w64(n > lo && before == r);
+    b_out = __builtin_ctzll(mine);
+    mt_out = lo;
+    return true;
+}
+
+// Sequence order.  Lane s counts the items of the sequences before it
+// (more M-tiles, or as many and an earlier index): its items hold ranks
+// [start_s, start_s + n_s), heaviest (highest M-tile) first.
+__device__ __forceinline__ bool sequence_item(const FmhaFwdParams& p, int rank, int& b_out, int& mt_out) {
+    const int lane = threadIdx.x & 63;
+    const int nseq = gridDim.z;
+    const int n = compact_ntiles(p);
+    int start = 0;
+    for (int s = 0; s < nseq; ++s) {
+        const int ns = __builtin_amdgcn_readlane(n, s);
+        start += (ns > n || (ns == n && s < lane)) ? ns : 0;
+    }
+    const uint64_t mine = __builtin_amdgcn_ballot_w64(start <= rank && rank < start + n);
+    if (mine == 0) return false;  // past the live items
+    const int b = __builtin_ctzll(mine);
+    b_out = b;
+    mt_out = __builtin_amdgcn_readlane(n, b) - 1 - (rank - __builtin_amdgcn_readlane(start, b));
+    return true;
+}
+
 }  // namespace fmha_gfx950
 
 using namespace fmha_gfx950;
@@ -1157,6 +1247,26 @@ FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_splitkv_msk1_tilemajor(FmhaFwdParams par
 FMHA_SPLIT_ATTRS void fmha_fwd_d64_bf16_pair_msk1_tilemajor(FmhaFwdParams params) {
     FMHA_RING(ring, kTileBytes)
     fwd_mtile<true, false, kModePair>(params, blockIdx.y, blockIdx.x, gridDim.z - 1 - blockIdx.z, ring);
+}
+
+// ---- compact causal varlen entries (this build's own; no counterpart in the
+// reference): the regular varlen grid (nhead_q, ceil(seqlen_q/kM0), batch) and
+// block, batch <= 64; the block of dispatch rank z * gridDim.y + y takes the
+// live (sequence, M-tile) item of that rank in the level order (highest
+// M-tile index first across all sequences) or the sequence order (longest
+// sequence first, each heaviest M-tile first); ranks past the live items
+// exit. ----
+FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen_tilemajor(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    int b, mt;
+    if (!level_item(params, (int)(blockIdx.z * gridDim.y + blockIdx.y), b, mt)) return;
+    fwd_mtile<true, true, kModeRegular>(params, b, blockIdx.x, mt, ring);
+}
+FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen_seqmajor(FmhaFwdParams params) {
+    FMHA_RING(ring, kTileBytes)
+    int b, mt;
+    if (!sequence_item(params, (int)(blockIdx.z * gridDim.y + blockIdx.y), b, mt)) return;
+    fwd_mtile<true, true, kModeRegular>(params, b, blockIdx.x, mt, ring);
 }
 
 // ---- balanced causal entries (this build's own; no counterpart in the

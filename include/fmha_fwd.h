@@ -137,9 +137,14 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
- * (every batch's heaviest M-tiles first) unless FMHA_VARIANT_REFERENCE_ORDER
- * is OR-ed into `variant`; the order changes no result bit.  An unknown
- * variant returns hipErrorInvalidValue. */
+ * (every batch's heaviest M-tiles first), and causal varlen launches of at
+ * most 64 sequences in the regular form a compact entry (the live M-tiles of
+ * all sequences, highest M-tile index first), unless one order flag is OR-ed
+ * into `variant`: FMHA_VARIANT_REFERENCE_ORDER (the reference's order),
+ * FMHA_VARIANT_TILE_MAJOR_ORDER (tile-major / level order wherever it
+ * exists) or FMHA_VARIANT_SEQUENCE_ORDER (varlen: longest sequence first);
+ * the order changes no result bit.  An unknown variant, or more than one
+ * order flag, returns hipErrorInvalidValue. */
 #define FMHA_VARIANT_AUTO 0
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
@@ -149,6 +154,10 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_SHORT 6
 #define FMHA_VARIANT_BALANCED_PAIR 7 /* fmha_fwd_d64_bf16_ws only: the balanced form over M-tile pairs */
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
+#define FMHA_VARIANT_TILE_MAJOR_ORDER 32 /* flag: causal dense batches on the tile-major entries (any K/V
+                                            size); causal varlen (regular form, <= 64 sequences): level order */
+#define FMHA_VARIANT_SEQUENCE_ORDER 64  /* flag: causal varlen (regular form, <= 64 sequences): sequence
+                                           order; dense batches as FMHA_VARIANT_REFERENCE_ORDER */
 hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int causal, int variant,
                                      hipStream_t stream);
 
@@ -226,10 +235,11 @@ hipError_t fmha_fwd_d64_bf16_check(const FmhaFwdParams* params, int batch, int c
  * arguments. */
 int fmha_fwd_d64_bf16_pick_variant(const FmhaFwdParams* params, int batch, int causal, int compute_units);
 
-/* 1 when a launch with these arguments (without FMHA_VARIANT_REFERENCE_ORDER)
- * runs a tile-major entry, 0 when it keeps the reference's order, -1 for
- * rejected arguments; host only (this build's own; no counterpart in the
- * reference). */
+/* The block order of the automatic launch (FMHA_VARIANT_AUTO, no order flag)
+ * with these arguments: 1 for a tile-major entry (causal dense batches) or the
+ * level order of a compact varlen entry, 2 for the sequence order of a
+ * compact varlen entry, 0 for the reference's order, -1 for rejected
+ * arguments; host only (this build's own; no counterpart in the reference). */
 int fmha_fwd_d64_bf16_tile_major(const FmhaFwdParams* params, int batch, int causal);
 
 /* Tile constants of the linked library, so FFI callers (ctypes, cgo) need not
@@ -315,6 +325,16 @@ __global__ void fmha_fwd_d64_bf16_short_msk1_varlen(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_msk1_tilemajor(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_splitkv_msk1_tilemajor(FmhaFwdParams params);
 __global__ void fmha_fwd_d64_bf16_pair_msk1_tilemajor(FmhaFwdParams params);
+/* Compact causal varlen forms (no counterpart in the reference): the grid and
+ * block of fmha_fwd_d64_bf16_msk1_varlen with at most 64 sequences (batch =
+ * grid z); the block of dispatch rank z * gridDim.y + y computes the live
+ * (sequence, M-tile) item of that rank, the items ordered by M-tile index,
+ * highest first, then by sequence (_tilemajor), or sequence after sequence,
+ * longest first, each heaviest M-tile first (_seqmajor); ranks past the live
+ * items do nothing.  Same results as fmha_fwd_d64_bf16_msk1_varlen, bit for
+ * bit. */
+__global__ void fmha_fwd_d64_bf16_msk1_varlen_tilemajor(FmhaFwdParams params);
+__global__ void fmha_fwd_d64_bf16_msk1_varlen_seqmajor(FmhaFwdParams params);
 #endif
 #endif /* __cplusplus */
 

@@ -90,14 +90,19 @@ def _params(prob, q, k, v, o, lse):
 
 
 NO_P_TRUNC = 1
+P_RNE_UNNORM = 2
+P_TRUNC_UNNORM = 4  # the kernel model with P truncated: a mistake tests plant in it
 
 
-def run(prob, q, k, v, *, faithful=False, nthreads=0, rows=None, p_trunc=True):
+def run(prob, q, k, v, *, faithful=False, nthreads=0, rows=None, p_trunc=True, kernel_model=False):
     """Oracle O (fp32, q's layout) and LSE (fp32, the kernel's LSE indexing).
 
     ``faithful``: the reference loop nest (slow); ``rows=(lo, hi)`` restricts
     it to those query rows of every (batch, head) (rows outside stay NaN).
     ``p_trunc=False``: skip the reference's bf16 truncation of P (fast form only).
+    ``kernel_model=True``: not the reference but a model of this build's
+    kernel's P rounding (nearest-even bf16 of the unnormalised P, fp32 row
+    sum), for tests that plant mistakes in it (fast form only).
     """
     nq, _, nlse = prob.sizes()
     o = np.full(nq, np.nan, dtype=np.float32)
@@ -110,8 +115,8 @@ def run(prob, q, k, v, *, faithful=False, nthreads=0, rows=None, p_trunc=True):
         rc = lib.oracle_fmha_fwd_faithful(ctypes.byref(p), prob.batch, int(prob.causal), nthreads, lo, hi)
     else:
         assert rows is None
-        rc = lib.oracle_fmha_fwd_ex(ctypes.byref(p), prob.batch, int(prob.causal), nthreads,
-                                    0 if p_trunc else NO_P_TRUNC)
+        flags = P_RNE_UNNORM if kernel_model else (0 if p_trunc else NO_P_TRUNC)
+        rc = lib.oracle_fmha_fwd_ex(ctypes.byref(p), prob.batch, int(prob.causal), nthreads, flags)
     if rc != 0:
         raise RuntimeError(f"oracle failed ({rc})")
     return o, lse

@@ -31,6 +31,12 @@
  *    step 5's bf16 truncation of P (the one quantisation the reference adds to
  *    imitate its kernel).  Its difference to the faithful result is the
  *    oracle's own truncation error, used as an explicit allowance in tests.
+ *  - oracle_fmha_fwd_ex(..., ORACLE_P_RNE_UNNORM): not the reference's
+ *    arithmetic but a model of this build's kernel (P = exp(s - m) rounded to
+ *    nearest-even bf16 before P.V, the row sum and the division by it in
+ *    fp32 on the unrounded P, O = (sum_j bf16(P_j) v_j) / sum_j P_j).  Tests
+ *    use it, on the CPU, to show that the parity bounds recorded for the
+ *    benchmark configurations fail when a mistake is planted in that model.
  *  - oracle_merge_d64(): the merge of partial results over disjoint key sets
  *    (no reference counterpart; it checks this build's fmha_merge_d64_bf16):
  *    LSE = log sum_i exp(LSE_i), O = sum_i exp(LSE_i - LSE) O_i in float64,
@@ -63,6 +69,8 @@ static inline uint16_t f32_to_bf16_trunc(float f) {
     memcpy(&u, &f, 4);
     return (uint16_t)(u >> 16);
 }
+
+static inline uint16_t f32_to_bf16_rne(float f);
 
 static int seq_lengths(const oracle_params* p, int b, int* sq, int* sk, int64_t* off_q, int64_t* off_k) {
     if (p->seqstart_q) {
@@ -235,7 +243,11 @@ static void row_fast(const oracle_params* p, int causal, int i, int sq, int sk, 
             sum += P[j];
         }
         float inv_sum = 1.0f / sum;
-        if (flags & ORACLE_NO_P_TRUNC)
+        if (flags & ORACLE_P_TRUNC_UNNORM)
+            for (int j = 0; j < n; j++) P[j] = bf16_to_f32(f32_to_bf16_trunc(P[j]));
+        else if (flags & ORACLE_P_RNE_UNNORM)
+            for (int j = 0; j < n; j++) P[j] = bf16_to_f32(f32_to_bf16_rne(P[j]));
+        else if (flags & ORACLE_NO_P_TRUNC)
             for (int j = 0; j < n; j++) P[j] = P[j] * inv_sum;
         else
             for (int j = 0; j < n; j++) P[j] = bf16_to_f32(f32_to_bf16_trunc(P[j] * inv_sum));
@@ -246,7 +258,10 @@ static void row_fast(const oracle_params* p, int causal, int i, int sq, int sk, 
             const float* vr = VF + (int64_t)j * D;
             for (int d = 0; d < D; d++) acc[d] += pj * vr[d];
         }
-        for (int d = 0; d < D; d++) orow[d] = acc[d];
+        if (flags & (ORACLE_P_RNE_UNNORM | ORACLE_P_TRUNC_UNNORM))
+            for (int d = 0; d < D; d++) orow[d] = acc[d] * inv_sum;
+        else
+            for (int d = 0; d < D; d++) orow[d] = acc[d];
     }
     if (lse_out) *lse_out = (sum > 0) ? logf(sum) + m : -INFINITY;
 }

@@ -39,6 +39,13 @@ int oracle_fmha_fwd_faithful(const oracle_params* p, int batch, int causal, int 
 int oracle_fmha_fwd(const oracle_params* p, int batch, int causal, int nthreads);
 /* flags: ORACLE_NO_P_TRUNC keeps P in fp32 (no bf16 truncation before P.V). */
 #define ORACLE_NO_P_TRUNC 1
+/* flags: ORACLE_P_RNE_UNNORM models this build's kernel instead of the
+ * reference: P rounded to nearest-even bf16 before normalisation, O divided by
+ * the fp32 row sum at the end. */
+#define ORACLE_P_RNE_UNNORM 2
+/* flags: the same model with P truncated instead of rounded (a mistake planted
+ * in the model by tests, to show that their parity bounds catch it). */
+#define ORACLE_P_TRUNC_UNNORM 4
 int oracle_fmha_fwd_ex(const oracle_params* p, int batch, int causal, int nthreads, int flags);
 /* float64 brute force (exact softmax, no P truncation); o64/lse64 use the
  * o / lse indexing of p. */

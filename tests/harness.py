@@ -102,6 +102,42 @@ def check_problem(prob, dist="ref", seed=42, mult=1.0, rule="reference", variant
     return res
 
 
+# Recorded parity of the benchmark configurations against the plain rule
+# (|O - O_ref| <= 1e-2 + 1e-2|O_ref|, O_ref the reference-faithful oracle):
+# (most violating elements, largest excess over the bound among them), per
+# configuration and kernel form.  cfg5 (inputs x2, a peaked softmax) is where
+# the oracle's own bf16 truncation of P (cpu_ref.cpp:137-144) reaches the
+# tolerance; its counts are those of the kernels as built (MI355X, one run of
+# each form; the results are deterministic) and a change that adds violations
+# fails.  Every other configuration passes the plain rule outright.
+CONTRACT_BOUNDS = {
+    "cfg5": {"auto": (15, 0.0059), "regular": (15, 0.0059), "pair": (15, 0.0059), "splitkv": (14, 0.0030),
+             "balanced": (15, 0.0059), "balanced_pair": (16, 0.0059), "short": (3, 0.0011)},
+}
+
+
+def contract_bound(cfg, form):
+    """(violations, excess) allowed for ``cfg`` in ``form`` (0, 0.0: none)."""
+    return CONTRACT_BOUNDS.get(cfg, {}).get(form, (0, 0.0))
+
+
+def contract_ok(res, bound):
+    """Whether a check_baseline result stays within a recorded bound: no more
+    plain-rule violations, no larger excess, and every violation explained by
+    the oracle's own P truncation (``o_unexplained == 0``)."""
+    n, excess = bound
+    return (res["o_plain"]["violations"] <= n and res["o_plain"]["max_excess"] <= excess
+            and res["o_unexplained"] == 0)
+
+
+def contract_counts(o_t, o_u, o_k):
+    """Plain rule against the faithful oracle ``o_t`` and the count of
+    violations not covered by that oracle's truncation error |o_t - o_u|."""
+    err = np.abs(o_k - o_t)
+    tol = 1e-2 + 1e-2 * np.abs(o_t) + np.abs(o_t - o_u)
+    return verify.baseline_rule(o_t, o_k), int(np.count_nonzero(~(err <= tol)))
+
+
 def check_baseline(prob, mult=1.0, seed=42, variant=0):
     """Benchmark-configuration check (N(0,1)*mult inputs).
 
@@ -117,11 +153,8 @@ def check_baseline(prob, mult=1.0, seed=42, variant=0):
     o_u, _ = oracle.run(prob, q, k, v, p_trunc=False)
     o_k = verify.bf16_bits_to_f32(o_bits)
     res = {"name": prob.name}
-    res["o_plain"] = verify.baseline_rule(o_t, o_k)
+    res["o_plain"], res["o_unexplained"] = contract_counts(o_t, o_u, o_k)
     res["o_vs_untruncated"] = verify.baseline_rule(o_u, o_k)
-    err = np.abs(o_k - o_t)
-    tol = 1e-2 + 1e-2 * np.abs(o_t) + np.abs(o_t - o_u)
-    res["o_unexplained"] = int(np.count_nonzero(~(err <= tol)))
     res["pass"] = res["o_vs_untruncated"]["pass"] and res["o_unexplained"] == 0
     if prob.lse:
         res["lse"] = verify.lse_rule(lse_t, lse)

@@ -30,7 +30,8 @@ KERNEL_ENTRIES = ["fmha_fwd_d64_bf16_msk0", "fmha_fwd_d64_bf16_msk1", "fmha_fwd_
                   "fmha_fwd_d64_bf16_msk1_varlen"]
 SPLIT_ENTRIES = [f"fmha_fwd_d64_bf16_{form}_msk{m}{v}" for form in ("splitkv", "pair") for m in (0, 1)
                  for v in ("", "_varlen")] + [f"fmha_fwd_d64_bf16_{f}msk1_tilemajor" for f in ("", "splitkv_", "pair_")] \
-    + [f"fmha_fwd_d64_bf16_short_msk{m}{v}" for m in (0, 1) for v in ("", "_varlen")]
+    + [f"fmha_fwd_d64_bf16_short_msk{m}{v}" for m in (0, 1) for v in ("", "_varlen")] \
+    + ["fmha_fwd_d64_bf16_msk1_varlen_tilemajor", "fmha_fwd_d64_bf16_msk1_varlen_seqmajor"]
 
 
 def header_c_functions():
@@ -193,9 +194,15 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    # 0-4 and 6 are the valid forms, optionally OR-ed with VARIANT_REFERENCE_ORDER (16)
-    for bad in (-1, 5, 7, 8, 32, 100, fmha.VARIANT_REFERENCE_ORDER | 7):  # 5: balanced needs the workspace entry
-        assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID
+    # 0-3 and 6 are the valid forms, optionally OR-ed with one order flag
+    # (VARIANT_REFERENCE_ORDER 16, VARIANT_TILE_MAJOR_ORDER 32, VARIANT_SEQUENCE_ORDER 64); 4 is retired,
+    # 5 and 7 (the balanced forms) need the workspace entry; two order flags at once are rejected
+    R, T, S = fmha.VARIANT_REFERENCE_ORDER, fmha.VARIANT_TILE_MAJOR_ORDER, fmha.VARIANT_SEQUENCE_ORDER
+    for bad in (-1, 4, 5, 7, 8, 100, 128, R | 7, T | 4, R | T, T | S, R | S, R | T | S, R | T | 1):
+        assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID, bad
+    for bad in (R | T, T | S | 2):
+        assert lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), 1, 1, bad, None, 0, None) == INVALID, bad
+        assert lib.fmha_fwd_d64_bf16_workspace_size(ctypes.byref(p), 1, 1, bad) == -1, bad
     bad_p = _mut(q=None)
     assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(bad_p), 1, 0, fmha.VARIANT_SPLITKV, None) == INVALID
 
@@ -291,11 +298,18 @@ def test_auto_form_rule(batch, heads, seqlen, causal, cus, form):
     (17, 16, 2, 2048, 1, False, 0),    # 8.5 MiB
     (1, 16, 16, 8192, 1, False, 0),    # one batch: nothing to interleave
     (8, 16, 16, 1024, 0, False, 0),    # dense: every block costs the same
-    (8, 16, 16, 1024, 1, True, 0),     # varlen keeps the reference's order
+    (8, 16, 16, 1024, 1, True, 1),     # varlen causal: the compact order (regular form, <= 64 sequences)
+    (64, 16, 16, 1024, 1, True, 1),
+    (65, 16, 16, 1024, 1, True, 0),    # more sequences than lanes: the reference's order
+    (8, 16, 16, 1024, 0, True, 0),     # varlen dense: the reference's order
+    (1, 8, 8, 4096, 1, True, 0),       # the split-KV form keeps the reference's order
+    (64, 16, 16, 128, 1, True, 0),     # so does the short form
 ])
 def test_tile_major_rule(batch, heads, kv_heads, seqlen, causal, varlen, expect):
     """Causal dense batches run tile-major while the K/V one XCD serves,
-    batch x ceil(nhead_k/8) x seqlen_k x 256 bytes, is at most 8 MiB."""
+    batch x ceil(nhead_k/8) x seqlen_k x 256 bytes, is at most 8 MiB; causal
+    varlen launches of at most 64 sequences in the regular form run the
+    compact order."""
     p = valid_params(lse=False)
     p.nhead_q, p.nhead_k = heads, kv_heads
     p.seqlen_q = p.seqlen_k = seqlen
