@@ -27,7 +27,7 @@ __all__ = [
     "tile_config", "pick_variant", "tile_major", "fill_ref", "fill_normal", "varlen_lengths", "params_from_tensors", "fmha_fwd",
     "fmha_merge_d64_bf16", "merge_partials", "MERGE_MAX_PARTS",
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
-    "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
+    "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "VARIANT_PAIR_STREAM", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANT_TILE_MAJOR_ORDER", "VARIANT_SEQUENCE_ORDER", "VARIANTS",
 ]
 
@@ -122,6 +122,7 @@ def load_library(path=LIB_PATH):
 VARIANT_AUTO, VARIANT_REGULAR, VARIANT_SPLITKV, VARIANT_PAIR, VARIANT_BALANCED = 0, 1, 2, 3, 5
 VARIANT_SHORT = 6
 VARIANT_BALANCED_PAIR = 7  # the balanced form over M-tile pairs (a workspace, like VARIANT_BALANCED)
+VARIANT_PAIR_STREAM = 8  # pair blocks looping over M-tile pairs (dense layouts only)
 # flag OR-ed into a variant: causal dense batches run batch after batch on the
 # reference's grid, never on the tile-major entries (results are identical)
 VARIANT_REFERENCE_ORDER = 16
@@ -131,7 +132,7 @@ VARIANT_TILE_MAJOR_ORDER = 32
 VARIANT_SEQUENCE_ORDER = 64
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
             "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
-            "balanced_pair": VARIANT_BALANCED_PAIR}
+            "balanced_pair": VARIANT_BALANCED_PAIR, "pair_stream": VARIANT_PAIR_STREAM}
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):

@@ -10,7 +10,7 @@
 //   --dist ref|normal   reference +-0.1 generator (default) or N(0,1)
 //   --scale-inputs X    multiply N(0,1) inputs by X
 //   --kv-seq N          key length (reference: always = seq)
-//   --variant auto|regular|splitkv|pair|balanced|balanced_pair|short   kernel form (default: the launcher's choice)
+//   --variant auto|regular|splitkv|pair|balanced|balanced_pair|short|pair_stream   kernel form (default: the launcher's choice)
 //   --workspace 0|1  give the launcher a workspace (fmha_fwd_d64_bf16_ws, allocated before timing), so the
 //                    automatic choice may be the balanced causal form (default 1); --variant balanced needs it
 //   --order auto|reference|tilemajor|sequence   causal block order (reference: batch after batch)
@@ -68,7 +68,7 @@ static void usage(const char* prog) {
            "  --seed N         Input seed [42]\n"
            "  --dist ref|normal  Input distribution [ref]\n"
            "  --scale-inputs X Multiplier for normal inputs [1]\n"
-           "  --variant V      auto|regular|splitkv|pair|balanced|balanced_pair|short form [auto]\n"
+           "  --variant V      auto|regular|splitkv|pair|balanced|balanced_pair|short|pair_stream form [auto]\n"
            "  --workspace 0|1  launch with a workspace (the balanced causal form may run) [1]\n"
            "  --order O        auto|reference|tilemajor|sequence causal block order [auto]\n",
            prog);
@@ -128,8 +128,9 @@ static Config parse(int argc, char** argv) {
                 else if (!strcmp(optarg, "balanced")) c.variant = FMHA_VARIANT_BALANCED;
                 else if (!strcmp(optarg, "balanced_pair")) c.variant = FMHA_VARIANT_BALANCED_PAIR;
                 else if (!strcmp(optarg, "short")) c.variant = FMHA_VARIANT_SHORT;
+                else if (!strcmp(optarg, "pair_stream")) c.variant = FMHA_VARIANT_PAIR_STREAM;
                 else {
-                    fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair, balanced, balanced_pair or short\n");
+                    fprintf(stderr, "Error: --variant must be auto, regular, splitkv, pair, balanced, balanced_pair, short or pair_stream\n");
                     exit(1);
                 }
                 break;

@@ -172,11 +172,21 @@ bool compact_applies(const FmhaFwdParams* p, int batch, int causal) {
     return causal && p->seqstart_q != nullptr && batch >= 1 && batch <= kCompactMaxSeqs;
 }
 // The varlen order of a regular-form causal launch: kOrderReference,
-// kOrderTileMajor (level order) or kOrderSequence.
+// kOrderTileMajor (level order) or kOrderSequence.  Automatic: the sequence
+// order for at most 8 sequences on a grid of at most 8 rounds of the resident
+// blocks (2 per CU), else the reference's.  Each block of a compact entry
+// finds its item in a loop over the sequences (~15 instructions each, in
+// dead blocks too), which the short M-tiles of many-sequence launches do not
+// repay.  Interleaved A/B in one process, H = nhead_q (reference order /
+// level / sequence): cfg4's eight lengths at H4 -3.6 % / +15 %, H8 +16 % /
+// +13 %, H16 -3.3 % / +2.2 %, H32 -15 % / -2.5 %; 16 lengths 100-4000 H8
+// +2.6 % / +5.1 %, H16 -12 % / -2.3 %; 32 and 64 sequences of 16-2048 tokens
+// H16 -17 to -29 % / -12 to -41 %; 16 x 512 H16 -1.1 % / -9.7 %.
 int varlen_order(const FmhaFwdParams* p, int batch, int causal, int order) {
     if (!compact_applies(p, batch, causal) || order == kOrderReference) return kOrderReference;
     if (order != kOrderAuto) return order;
-    return kOrderTileMajor;
+    const int64_t blocks = (int64_t)p->nhead_q * ((p->seqlen_q + kM0 - 1) / kM0) * batch;  // the grid: a bound
+    return batch <= 8 && blocks <= 16 * (int64_t)device_cus() ? kOrderSequence : kOrderReference;
 }
 // Dense causal batches on the tile-major entries?
 bool dense_tile_major(const FmhaFwdParams* p, int batch, int causal, int order) {
@@ -471,13 +481,34 @@ extern "C" hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* p, int batc
     const bool tile_major = dense_tile_major(p, batch, causal, order);
     variant &= ~kOrderFlags;
     // the balanced forms need fmha_fwd_d64_bf16_ws; 4 is a retired value
-    if (variant < FMHA_VARIANT_AUTO || variant > FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_BALANCED ||
-        variant == 4)
+    if (!(variant == FMHA_VARIANT_AUTO || variant == FMHA_VARIANT_REGULAR || variant == FMHA_VARIANT_SPLITKV ||
+          variant == FMHA_VARIANT_PAIR || variant == FMHA_VARIANT_SHORT || variant == FMHA_VARIANT_PAIR_STREAM))
         return hipErrorInvalidValue;
     const bool varlen = p->seqstart_q != nullptr;
+    if (variant == FMHA_VARIANT_PAIR_STREAM && varlen) return hipErrorInvalidValue;  // dense layouts only
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;  // nothing to compute
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
     const dim3 grid(p->nhead_q, m_tiles, batch);
+    if (variant == FMHA_VARIANT_PAIR_STREAM) {
+        // one block per compute unit over the pairs (dense), or one per pair
+        // and its mirror (causal)
+        const int64_t ny = (m_tiles + 1) / 2;
+        const int64_t items = (int64_t)p->nhead_q * ny * batch;
+        if (items >= INT32_MAX) return hipErrorInvalidValue;  // item numbers are ints
+        const int64_t blocks = causal ? (int64_t)p->nhead_q * ((ny + 1) / 2) * batch
+                                      : std::min<int64_t>(items, device_cus());
+        FmhaStreamArgs a;
+        a.p = *p;
+        a.ny = (int)ny;
+        a.n_items = (int)items;
+        if (causal)
+            hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_stream_msk1, dim3((unsigned)blocks), dim3(FMHA_SPLIT_KBLOCK), 0,
+                               stream, a);
+        else
+            hipLaunchKernelGGL(fmha_fwd_d64_bf16_pair_stream_msk0, dim3((unsigned)blocks), dim3(FMHA_SPLIT_KBLOCK), 0,
+                               stream, a);
+        return hipGetLastError();
+    }
     if (variant == FMHA_VARIANT_AUTO)
         variant = pick_form(p, batch, causal, device_cus());
     if (variant == FMHA_VARIANT_SHORT) {

@@ -108,6 +108,11 @@ struct Ring {
 __device__ __forceinline__ void lds_dma_16(__amdgpu_buffer_rsrc_t rsrc, lds_char* dst, int voffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, voffset, 0, 0, 0);
 }
+// The same with a wave-uniform byte offset in the scalar offset operand.
+__device__ __forceinline__ void lds_dma_16(__amdgpu_buffer_rsrc_t rsrc, lds_char* dst, int voffset, int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset,
+                                             0, 0);
+}
 // Own-wave DMA completion before a tile barrier (the barrier then makes every
 // wave's part of the tile visible).
 template <int N>
@@ -784,6 +789,510 @@ __device__ __forceinline__ void fwd_mtile(const FmhaFwdParams& p, int b, int h, 
 }
 
 // ===========================================================================
+// Pair stream form (this build's own; no counterpart in the reference).
+//
+// The pair form's 8-wave block is alone on its compute unit, so nothing
+// hides its prologue (the first Q and K/V tiles from memory, GEMM0 of the
+// first tile) or its epilogue (O through LDS to memory): a launch of two
+// rounds of pair blocks pays both twice per CU.  Here one pair block per CU
+// loops over a static list of M-tile pairs and its K/V ring runs on from one
+// pair into the next: the next pair's first K/V tiles are fetched during the
+// current pair's last four iterations and its Q rows arrive by LDS-DMA (in
+// the current pair's second iteration) into a 4 KiB buffer per wave, read
+// into the GEMM0 operand for the last iteration (whose GEMM0 is the next
+// pair's first tile); the current pair's
+// last GEMM1 and its epilogue run in the next pair's first iteration, the O
+// tile staged through the same buffer.
+//
+// Items are the pair grid's blocks (head fastest, then pair, then batch).
+// Dense: block i takes items i, i + G, i + 2G, ... below n_items (G =
+// gridDim.x; every item has the same key tiles).  Causal: block i takes
+// pair Y-1-y of its (batch, head) and then its mirror y (Y pairs per
+// (batch, head); the middle pair of an odd Y alone), so the blocks' key
+// tiles balance and each block's two pairs read the same K/V.  With G a
+// multiple of 8 and of nhead_q a head's items all run on the XCD of its
+// blocks, as in the pair grid.  Every item runs a multiple of 4 ring
+// iterations (the ring stages stay compile-time), at least 8 (the
+// successor's fetches in the last four never meet the predecessor's GEMM1
+// in the first); the padding iterations see zero-filled, fully masked tiles.
+// ===========================================================================
+typedef __attribute__((address_space(4))) const FmhaStreamArgs* SArgsPtr;
+
+// The kernarg block through a pointer the compiler cannot follow across
+// calls of this function: loads through the result are issued where they
+// are used instead of being held in SGPRs across the inner loop.
+__device__ __forceinline__ SArgsPtr sargs_here() {
+    SArgsPtr ap = (SArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    return ap;
+}
+
+// Items this block runs (wave-uniform).
+template <bool kCausal>
+__device__ __forceinline__ int stream_items(SArgsPtr ap) {
+    if constexpr (kCausal) {
+        const int ny = ap->ny, half = (ny + 1) >> 1;
+        const int y = (int)(blockIdx.x / ap->p.nhead_q) % half;
+        return 2 * y + 1 == ny ? 1 : 2;
+    } else {
+        return (ap->n_items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    }
+}
+
+// Item k of this block: batch b, head h, pair pr (wave-uniform).
+template <bool kCausal>
+__device__ __forceinline__ void stream_coords(SArgsPtr ap, int k, int& b, int& h, int& pr) {
+    const int nh = ap->p.nhead_q, ny = ap->ny;
+    if constexpr (kCausal) {
+        const int half = (ny + 1) >> 1;
+        const int i = blockIdx.x;
+        h = i % nh;
+        const int r = i / nh;
+        const int y = r % half;
+        b = r / half;
+        pr = k == 0 ? ny - 1 - y : y;  // the heavy pair, then its mirror
+    } else {
+        const int L = blockIdx.x + k * gridDim.x;
+        h = L % nh;
+        const int r = L / nh;
+        pr = r % ny;
+        b = r / ny;
+    }
+}
+
+// What the K/V ring needs of an item (wave-uniform): the first K and V row
+// of its (batch, KV head), the pair's first query row, its key tiles (those
+// of its last row) and its ring iterations.  A dead item has no tiles (its
+// loads are zero fills).
+struct StreamKV {
+    const char* k;
+    const char* v;
+    int row0;
+    int ntiles;
+    int npad;
+};
+template <bool kCausal>
+__device__ __forceinline__ StreamKV stream_kv(SArgsPtr ap, int k, bool valid) {
+    int b, h, pr;
+    stream_coords<kCausal>(ap, valid ? k : 0, b, h, pr);
+    const int sq = ap->p.seqlen_q, sk = ap->p.seqlen_k;
+    int kv_end = sk;
+    if constexpr (kCausal) {  // pipeline.hpp:168-193, over the pair's last row
+        const int last = min(2 * pr * kTileM + 2 * kTileM - 1, sq - 1);
+        const int e = last + (sk - sq) + 1;
+        kv_end = e < 0 ? 0 : (e > sk ? sk : e);
+    }
+    StreamKV it;
+    it.row0 = 2 * pr * kTileM;
+    it.ntiles = valid ? (kv_end + kTileN - 1) / kTileN : 0;
+    it.npad = max(2 * kRing, (it.ntiles + kRing - 1) & ~(kRing - 1));
+    const int kvh = h / (ap->p.nhead_q / ap->p.nhead_k);
+    it.k = (const char*)(ap->p.k + (int64_t)b * ap->p.batch_stride_k + (int64_t)kvh * ap->p.nhead_stride_k);
+    it.v = (const char*)(ap->p.v + (int64_t)b * ap->p.batch_stride_v + (int64_t)kvh * ap->p.nhead_stride_v);
+    return it;
+}
+
+template <bool kCausal>
+__device__ __forceinline__ void fwd_pair_stream(const Ring& ring, lds_char* qbuf) {
+    const int lane = threadIdx.x & 63;
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 0-7
+    const int group = wave_id / kWaves;                                    // the pair's M-tile
+    const int wave = wave_id % kWaves;                                     // 32 rows of it
+    const int l32 = lane & 31;
+    const int hi = lane >> 5;
+
+    // per-lane constants (VGPRs), as the pair form: each wave moves 1 KiB
+    // (rows 8 * wave_id .. +7) of every K and V tile
+    int k_ld_off, v_ld_off;
+    // Q DMA: load i brings rows 8i + lane/8 of this wave's 32, physical chunk
+    // lane%8 holding logical chunk (lane%8) ^ k_swz(8i + lane/8) =
+    // (lane%8) ^ (lane/8) ^ (i&1); the offsets of even and odd i
+    int q_ld_off[2];
+    {
+        SArgsPtr ap = sargs_here();
+        const int ld_row = wave_id * 8 + (lane >> 3);
+        const int ld_pc = lane & 7;
+        k_ld_off = ld_row * ap->p.stride_k * 2 + ((ld_pc ^ k_swz(ld_row)) << 4);
+        v_ld_off = ld_row * ap->p.stride_v * 2 + ((ld_pc ^ v_swz(ld_row)) << 4);
+        const int q_row = wave * kRowsPerWave + (lane >> 3);
+        const int sw = (lane & 7) ^ (lane >> 3);
+        q_ld_off[0] = q_row * ap->p.stride_q * 2 + (sw << 4);
+        q_ld_off[1] = q_row * ap->p.stride_q * 2 + ((sw ^ 1) << 4);
+    }
+    const int wave_off = wave_id * 1024;
+    // this wave's 32 Q rows of the next item, swizzled as K rows (the GEMM0 B
+    // operand is read with the K read pattern); also the O staging of the
+    // epilogue
+    lds_char* const qw = qbuf + wave_id * (kRowsPerWave * kRowBytes);
+
+    uint32_t k_rd[4];
+    {
+        const int f = k_swz(l32);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) k_rd[t] = l32 * kRowBytes + (((2 * t + hi) ^ f) << 4);
+    }
+    uint32_t v_rd[2];
+    {
+        const int g = lane >> 4, i16 = lane & 15;
+        const int e = i16 >> 2, c = i16 & 3;
+        const int row = 4 * hi + e;
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
+            v_rd[db] = row * kRowBytes + ((chunk ^ v_swz(row)) << 4) + (c & 1) * 8;
+        }
+    }
+
+    bf16x8 qop[4];
+    f32x16 oacc[2];
+    f32x16 sacc[2][2];
+    bf16x8 pbuf[2][4];
+    Softmax sm{kMaxSeed, 0.0f, 0.0f};
+    Softmax smz{kMaxSeed, 0.0f, 0.0f};  // the previous item's, until its epilogue
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
+
+    // the item in progress (number KX of this block, ring view X), its
+    // successor (KX + 1) and its predecessor (KX - 1, whose last GEMM1 and
+    // epilogue run in X's iteration 0)
+    int KX = 0;
+    const int n_mine = stream_items<kCausal>(sargs_here());
+    StreamKV X;
+    int sk, shift;
+    uint32_t kbytes, vbytes;
+    int k_tile_step, v_tile_step;
+    float scale, scale_v;
+    auto load_item = [&]() {  // X's view and the per-launch constants, reloaded per item
+        SArgsPtr ap = sargs_here();
+        X = stream_kv<kCausal>(ap, KX, true);
+        sk = ap->p.seqlen_k;
+        shift = sk - ap->p.seqlen_q;
+        kbytes = sk > 0 ? (uint32_t)((int64_t)(sk - 1) * ap->p.stride_k * 2 + kRowBytes) : 0u;
+        vbytes = sk > 0 ? (uint32_t)((int64_t)(sk - 1) * ap->p.stride_v * 2 + kRowBytes) : 0u;
+        k_tile_step = kTileN * ap->p.stride_k * 2;
+        v_tile_step = kTileN * ap->p.stride_v * 2;
+        scale = ap->p.scale;
+        scale_v = in_vgpr(scale);
+    };
+
+    // DMA of tile `tile` (K or V) of the item `view` into stage S
+    auto issue_k = [&](const StreamKV& view, int tile, auto stage_c) {
+        lds_char* dst = ring.k[decltype(stage_c)::value] + wave_off;
+        const uint32_t t0 = (uint32_t)tile * (uint32_t)k_tile_step;
+        lds_dma_16(make_rsrc(view.k + t0, tile < view.ntiles ? kbytes - t0 : 0u), dst, k_ld_off);
+    };
+    auto issue_v = [&](const StreamKV& view, int tile, auto stage_c) {
+        lds_char* dst = ring.v[decltype(stage_c)::value] + wave_off;
+        const uint32_t t0 = (uint32_t)tile * (uint32_t)v_tile_step;
+        lds_dma_16(make_rsrc(view.v + t0, tile < view.ntiles ? vbytes - t0 : 0u), dst, v_ld_off);
+    };
+    // this wave's 32 Q rows of item k into its Q buffer (q_ld_off); past the
+    // block's last item, zeros (an empty descriptor).  Issued on every path:
+    // a branch around it would leave the compiler's wait placement with two
+    // load counts to merge, and it then waits for the prefetch in flight.
+    auto issue_q = [&](int k) {
+        SArgsPtr ap = sargs_here();
+        const bool valid = k < n_mine;
+        int b, h, pr;
+        stream_coords<kCausal>(ap, valid ? k : 0, b, h, pr);
+        const int sq = ap->p.seqlen_q, sq_stride = ap->p.stride_q;
+        const uint32_t qbytes = sq > 0 ? (uint32_t)((int64_t)(sq - 1) * sq_stride * 2 + kRowBytes) : 0u;
+        const char* q = (const char*)(ap->p.q + (int64_t)b * ap->p.batch_stride_q + (int64_t)h * ap->p.nhead_stride_q);
+        const uint32_t r0 = (uint32_t)(2 * pr * kTileM + group * kTileM) * (uint32_t)(sq_stride * 2);
+        // wave-uniform (a saturating subtract would otherwise land in a VGPR
+        // and the DMA in a loop over its lanes' values)
+        const uint32_t nrec = __builtin_amdgcn_readfirstlane(valid && qbytes > r0 ? qbytes - r0 : 0u);
+        const auto r = make_rsrc(q + r0, nrec);
+        // the per-lane offsets are loop-invariant registers (q_ld_off), the
+        // load's 8-row step a scalar: the compiler keeps a DMA's offset
+        // register reserved until the DMA completes, and would wait for it
+        // before reusing a temporary
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_dma_16(r, qw + i * 1024, q_ld_off[i & 1], i * 8 * sq_stride * 2);
+    };
+    auto gemm0 = [&](auto ks_c, f32x16* s) {
+        const lds_char* st = ring.k[decltype(ks_c)::value];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x16 acc = {};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc = mfma(lds_read_b128(st + k_rd[k] + kb * 32 * kRowBytes), qop[k], acc);
+            s[kb] = acc;
+        }
+    };
+    auto gemm1 = [&](auto vs_c, const bf16x8* pp) {
+        const lds_char* st = ring.v[decltype(vs_c)::value];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    oacc[db] = mfma(lds_read_vt(st + v_rd[db] + (kb * 32 + 16 * k) * kRowBytes), pp[2 * kb + k],
+                                    oacc[db]);
+    };
+    // X's tile t: keys >= sk, and (causal) keys > row + shift
+    auto mask_tile = [&](int t, f32x16* s) {
+        const int key0 = t * kTileN;
+        const int wrow0 = X.row0 + group * kTileM + wave * kRowsPerWave;
+        const bool need = (key0 + kTileN > sk) || (kCausal && key0 + kTileN - 1 > wrow0 + shift);
+        if (need) {
+            const int lim = kCausal ? min(sk - 1, wrow0 + l32 + shift) : sk - 1;
+            const int d = lim - (key0 + 4 * hi);
+            const float ninf = in_vgpr(-__builtin_inff());
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                    s[kb][r] = c <= d ? s[kb][r] : ninf;
+                }
+        }
+    };
+    auto tile_max = [&](const f32x16* s) {
+        float mp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mp[i] = fmaxf(fmaxf(s[i >> 2][4 * (i & 3)], s[i >> 2][4 * (i & 3) + 1]),
+                                                  fmaxf(s[i >> 2][4 * (i & 3) + 2], s[i >> 2][4 * (i & 3) + 3]));
+        const float mx = fmaxf(fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3])),
+                               fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7])));
+        return wave_max_halves(mx);
+    };
+    auto exp_tile = [&](const f32x16* s, bf16x8* pp) {
+        const float neg_ms = -sm.m_ref;
+        float ls[4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                bf16x8 pk;
+                float acc;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 * k + e], scale_v, neg_ms));
+                    acc = e == 0 ? pv : acc + pv;
+                    pk[e] = (__bf16)pv;
+                }
+                ls[2 * kb + k] = acc;
+                pp[2 * kb + k] = pk;
+            }
+        sm.l_tile = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+    auto softmax = [&](const f32x16* s, bf16x8* pp) {
+        exp_tile(s, pp);
+        asm volatile("" ::"v"(pp[0]), "v"(pp[1]), "v"(pp[2]), "v"(pp[3]), "v"(sm.l_tile));
+    };
+    auto settle = [&](const f32x16* s, bf16x8* pp) {
+        if (__builtin_amdgcn_ballot_w64(!(sm.l_tile <= kGrowSum))) {
+            asm volatile("" ::: "memory");
+            const float m_new = fmaxf(sm.m_ref, tile_max(s) * scale);
+            const float alpha = __builtin_amdgcn_exp2f(sm.m_ref - m_new);
+            sm.m_ref = m_new;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+            sm.l_part *= alpha;
+            exp_tile(s, pp);
+        }
+        sm.l_part += sm.l_tile;
+    };
+    // O = O^T / l and LSE of item k (softmax state `st`), staged through this
+    // wave's Q buffer as the regular form's epilogue stages through a K stage
+    auto epilogue = [&](int k, const Softmax& st) {
+        SArgsPtr ap = sargs_here();
+        int b, h, pr;
+        stream_coords<kCausal>(ap, k, b, h, pr);
+        const int sq = ap->p.seqlen_q, so = ap->p.stride_o;
+        const float l_tot = wave_sum_halves(st.l_part);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const uint32_t obytes = (uint32_t)((int64_t)(sq - 1) * so * 2 + kRowBytes);
+        const auto ro = make_rsrc(ap->p.o + (int64_t)b * ap->p.batch_stride_o + (int64_t)h * ap->p.nhead_stride_o,
+                                  obytes);
+        const int wrow0 = 2 * pr * kTileM + group * kTileM + wave * kRowsPerWave;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                bf16x2 x0, x1;
+                x0[0] = (__bf16)(oacc[db][4 * g4 + 0] * inv);
+                x0[1] = (__bf16)(oacc[db][4 * g4 + 1] * inv);
+                x1[0] = (__bf16)(oacc[db][4 * g4 + 2] * inv);
+                x1[1] = (__bf16)(oacc[db][4 * g4 + 3] * inv);
+                i32x2 w;
+                w[0] = __builtin_bit_cast(int, x0);
+                w[1] = __builtin_bit_cast(int, x1);
+                const int c = 4 * db + g4;
+                *(lds_i32x2*)(qw + l32 * kRowBytes + ((c ^ ((l32 >> 1) & 7)) << 4) + 8 * (hi ^ (l32 & 1))) = w;
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / 8; ++i) {
+            const int r = 8 * i + (lane >> 3), pc = lane & 7;
+            const i32x4 raw = *(const lds_i32x4*)(qw + r * kRowBytes + (pc << 4));
+            const i32x4 v = (r & 1) ? i32x4{raw[2], raw[3], raw[0], raw[1]} : raw;
+            const int c = pc ^ ((r >> 1) & 7);
+            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wrow0 + r) * so * 2 + c * 16, 0, kStoreStream);
+        }
+        const int my_row = wrow0 + l32;
+        float* const lse = ap->p.lse;
+        if (lse != nullptr && hi == 0 && my_row < sq) {
+            const float lse2 = __builtin_log2f(l_tot) + st.m_ref;  // -inf when l == 0
+            lse[(int64_t)b * ap->p.nhead_q * sq + (int64_t)h * sq + my_row] = lse2 * 0.69314718055994530942f;
+        }
+        // the staging reads must be done before this buffer takes Q rows again
+        // (the successor's Q DMA in the next iteration)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
+
+    // one ring iteration t of X (phase J = t % 4): GEMM1(t-1) || GEMM0(t+1)
+    // || softmax(t); its K(t+4) and V(t+2) DMAs come from `kv`/`vv` (X's view,
+    // or the successor's in the last four iterations, with the tile counted
+    // from it).  The wait lets the two previous iterations' loads fly (W = 4)
+    // and, in iterations 2 and 3, the successor's Q DMA issued in iteration 1
+    // too (W = 8); `q_next`: iteration 1, which issues that DMA first.
+    auto iteration = [&](int t, auto phase_c, const StreamKV& kv, int kt, const StreamKV& vv, int vt,
+                         auto wait_c, auto q_next) {
+        constexpr int J = decltype(phase_c)::value;
+        constexpr int cur = J & 1, nxt = cur ^ 1;
+        vmcnt_wait<decltype(wait_c)::value>();  // K(t+1) and V(t-1) landed
+        ring_barrier();
+        if constexpr (decltype(q_next)::value) issue_q(KX + 1);
+        issue_k(kv, kt, std::integral_constant<int, J>{});
+        issue_v(vv, vt, std::integral_constant<int, (J + 2) % kRing>{});
+        mask_tile(t, sacc[cur]);
+        gemm1(std::integral_constant<int, (J + kRing - 1) % kRing>{}, pbuf[nxt]);
+        gemm0(std::integral_constant<int, (J + 1) % kRing>{}, sacc[nxt]);
+        softmax(sacc[cur], pbuf[cur]);
+        IterSchedule<true, true>::apply();
+        settle(sacc[cur], pbuf[cur]);
+    };
+    using W4 = std::integral_constant<int, 4>;
+    using W8 = std::integral_constant<int, 8>;
+    using NoQ = std::false_type;
+    auto mid = [&](int t, auto phase_c) { iteration(t, phase_c, X, t + kRing, X, t + 2, W4{}, NoQ{}); };
+
+    // iteration 0 of X: X's frame from its first tile's exact max; GEMM1 of
+    // the predecessor's last tile (kPrev), whose epilogue follows
+    auto first = [&](auto prev_c) {
+        constexpr bool kPrev = decltype(prev_c)::value;
+        vmcnt_wait<4>();
+        ring_barrier();
+        issue_k(X, kRing, P0{});
+        issue_v(X, 2, P2{});
+        mask_tile(0, sacc[0]);
+        sm.m_ref = fmaxf(kMaxSeed, tile_max(sacc[0]) * scale);
+        if constexpr (kPrev) gemm1(P3{}, pbuf[1]);
+        gemm0(P1{}, sacc[1]);
+        softmax(sacc[0], pbuf[0]);
+        IterSchedule<kPrev, true>::apply();
+        sm.l_part = sm.l_tile;  // exact frame: nothing to re-frame
+        if constexpr (kPrev) {
+            epilogue(KX - 1, smz);
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
+        }
+    };
+    // X's last four iterations: K(t+4) is the successor's tile t+4-npad, V(t+2)
+    // too from npad-2 on; the successor's Q rows, in the Q buffer since
+    // iteration 1, go into qop before the last iteration's GEMM0 (its first
+    // tile); past the block's last item the successor is dead (zero tiles,
+    // no Q)
+    auto tail = [&]() {
+        const int t = X.npad - kRing;
+        const bool has_next = KX + 1 < n_mine;
+        const StreamKV N = stream_kv<kCausal>(sargs_here(), KX + 1, has_next);
+        iteration(t, P0{}, N, 0, X, t + 2, W4{}, NoQ{});
+        iteration(t + 1, P1{}, N, 1, X, t + 3, W4{}, NoQ{});
+        iteration(t + 2, P2{}, N, 2, N, 0, W4{}, NoQ{});
+        {
+            vmcnt_wait<4>();
+            ring_barrier();
+            issue_k(N, 3, P3{});
+            issue_v(N, 1, P1{});
+            // the successor's Q (zeros past the block's last item, whose
+            // GEMM0 result below is then unused)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qop[k] = lds_read_b128(qw + k_rd[k]);
+            mask_tile(t + 3, sacc[1]);
+            gemm1(P2{}, pbuf[0]);
+            gemm0(P0{}, sacc[0]);
+            softmax(sacc[1], pbuf[1]);
+            IterSchedule<true, true>::apply();
+            settle(sacc[1], pbuf[1]);
+        }
+        return has_next;
+    };
+
+    load_item();
+    // prologue of the block's first item: Q straight into registers, K0 K1
+    // V0 K2 V1 K3 in flight, GEMM0 of tile 0 once Q and K0 landed
+    {
+        SArgsPtr ap = sargs_here();
+        int b, h, pr;
+        stream_coords<kCausal>(ap, 0, b, h, pr);
+        const int sq = ap->p.seqlen_q;
+        const uint32_t qbytes = sq > 0 ? (uint32_t)((int64_t)(sq - 1) * ap->p.stride_q * 2 + kRowBytes) : 0u;
+        const auto rq = make_rsrc(ap->p.q + (int64_t)b * ap->p.batch_stride_q + (int64_t)h * ap->p.nhead_stride_q,
+                                  qbytes);
+        const int qoff = (X.row0 + group * kTileM + wave * kRowsPerWave + l32) * ap->p.stride_q * 2 + hi * 16;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + t * 32, 0, 0);
+            qop[t] = __builtin_bit_cast(bf16x8, raw);
+        }
+    }
+    issue_k(X, 0, P0{});
+    issue_k(X, 1, P1{});
+    issue_v(X, 0, P0{});
+    issue_k(X, 2, P2{});
+    issue_v(X, 1, P1{});
+    issue_k(X, 3, P3{});
+    vmcnt_wait<5>();  // the Q loads (issued first) and K0 have landed
+    ring_barrier();
+    asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
+    gemm0(P0{}, sacc[0]);
+    bool prev = false;
+    while (true) {
+        if (prev)
+            first(std::true_type{});
+        else
+            first(std::false_type{});
+        // iteration 1 issues the successor's Q DMA before its K/V loads (on
+        // every path: see issue_q); the waits of iterations 2 and 3 let those
+        // four loads fly too (iteration 4's wait retires them)
+        iteration(1, P1{}, X, 1 + kRing, X, 1 + 2, W4{}, std::true_type{});
+        iteration(2, P2{}, X, 2 + kRing, X, 2 + 2, W8{}, NoQ{});
+        iteration(3, P3{}, X, 3 + kRing, X, 3 + 2, W8{}, NoQ{});
+        for (int t = kRing; t < X.npad - kRing; t += kRing) {
+            mid(t, P0{});
+            mid(t + 1, P1{});
+            mid(t + 2, P2{});
+            mid(t + 3, P3{});
+        }
+        if (!tail()) break;
+        smz = sm;
+        ++KX;
+        load_item();
+        prev = true;
+    }
+    // drain: the last item's last GEMM1 and its epilogue
+    vmcnt_wait<0>();
+    ring_barrier();
+    gemm1(P3{}, pbuf[1]);
+    epilogue(KX, sm);
+}
+
+// ===========================================================================
 // Short form (this build's own; no counterpart in the reference): the
 // regular grid at four blocks per compute unit (<= 128 VGPRs and 32 KiB of
 // LDS; the regular form fits two), for launches whose M-tiles see few key
@@ -1267,6 +1776,26 @@ FMHA_ENTRY_ATTRS void fmha_fwd_d64_bf16_msk1_varlen_seqmajor(FmhaFwdParams param
     int b, mt;
     if (!sequence_item(params, (int)(blockIdx.z * gridDim.y + blockIdx.y), b, mt)) return;
     fwd_mtile<true, true, kModeRegular>(params, b, blockIdx.x, mt, ring);
+}
+
+// ---- pair stream entries (this build's own; no counterpart in the
+// reference): one block of 2*kBlockSize threads per compute unit (grid
+// (blocks)), each looping over M-tile pairs; 96 KiB of LDS (the K/V rings and
+// a 4 KiB Q/O buffer per wave).  Launched by the C-ABI only. ----
+#define FMHA_STREAM_ATTRS \
+    __global__ __launch_bounds__(FMHA_SPLIT_KBLOCK) __attribute__((amdgpu_waves_per_eu(2, 2)))
+constexpr int kStreamQBytes = 2 * kWaves * kRowsPerWave * kRowBytes;  // 32 KiB: 4 KiB per wave
+FMHA_STREAM_ATTRS void fmha_fwd_d64_bf16_pair_stream_msk0(FmhaStreamArgs args) {
+    FMHA_RING(ring, kTileBytes)
+    __shared__ __attribute__((aligned(1024))) char qbuf[kStreamQBytes];
+    (void)args;  // read through the kernarg segment pointer
+    fwd_pair_stream<false>(ring, (lds_char*)qbuf);
+}
+FMHA_STREAM_ATTRS void fmha_fwd_d64_bf16_pair_stream_msk1(FmhaStreamArgs args) {
+    FMHA_RING(ring, kTileBytes)
+    __shared__ __attribute__((aligned(1024))) char qbuf[kStreamQBytes];
+    (void)args;
+    fwd_pair_stream<true>(ring, (lds_char*)qbuf);
 }
 
 // ---- balanced causal entries (this build's own; no counterpart in the

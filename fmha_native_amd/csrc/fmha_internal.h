@@ -23,3 +23,13 @@ struct FmhaBalancedArgs {
 __global__ void fmha_fwd_d64_bf16_balanced_msk1(FmhaBalancedArgs args);
 __global__ void fmha_fwd_d64_bf16_balanced_pair_msk1(FmhaBalancedArgs args);
 __global__ void fmha_fwd_d64_bf16_balanced_merge(FmhaBalancedArgs args);
+
+// Pair stream form (see fmha_fwd_kernel.hip): one 8-wave pair block per
+// compute unit looping over a static list of M-tile pairs.
+struct FmhaStreamArgs {
+    FmhaFwdParams p;
+    int ny;       // pairs per (batch, head): ceil(ceil(seqlen_q / kM0) / 2)
+    int n_items;  // pairs of the launch: nhead_q * ny * batch
+};
+__global__ void fmha_fwd_d64_bf16_pair_stream_msk0(FmhaStreamArgs args);
+__global__ void fmha_fwd_d64_bf16_pair_stream_msk1(FmhaStreamArgs args);

@@ -242,8 +242,8 @@ def profile_forms(args):
                f"{line['tflops']:.1f} TFLOP/s ({100 * line['tflops'] / PEAK_BF16_TFLOPS:.1f}% of 2516.6)"
                + (f"; exact-count {prob.exact_flops() / (line['ms_per_step'] * 1e-3) / 1e12:.1f} TFLOP/s"
                   if prob.varlen else "") + ".", "",
-               "| kernel | dispatches | trace avg, timed (all) | clock ≥ | MFMA busy | fraction of peak | "
-               "VGPR / AGPR / SGPR | LDS bytes |", "|---|---|---|---|---|---|---|---|"]
+               "| kernel | dispatches | trace avg, timed (all) | active cycles | clock ≥ | MFMA busy | "
+               "fraction of peak | VGPR / AGPR / SGPR | LDS bytes |", "|---|---|---|---|---|---|---|---|---|"]
         entry = {"bench": line, "trace_step_us": round(step_us, 3),
                  "trace_tflops": round(flops / (step_us * 1e-6) / 1e12, 2), "kernels": {}}
         for k in ks:
@@ -255,17 +255,19 @@ def profile_forms(args):
                 # a dispatch this short is mostly set-up and drain: clock and
                 # busy are not meaningful for it
                 md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | — | — | — | "
-                          f"{c['vgpr']} / {c['agpr']} / {c['sgpr']} | {c['lds_bytes']} |")
+                          f"— | {c['vgpr']} / {c['agpr']} / {c['sgpr']} | {c['lds_bytes']} |")
             else:
-                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | {ghz:.3f} GHz | "
+                md.append(f"| `{k['name']}` | {k['calls']} | {k['avg_us']:.2f} ({k['avg_all_us']:.2f}) us | "
+                          f"{c['SQ_BUSY_CYCLES'] / n_se / 1e3:.1f}k | {ghz:.3f} GHz | "
                           f"{100 * busy:.1f}% | {100 * frac:.1f}% | {c['vgpr']} / {c['agpr']} / {c['sgpr']} | "
                           f"{c['lds_bytes']} |")
             entry["kernels"][k["name"]] = {"trace_avg_us": round(k["avg_us"], 3), "calls": k["calls"],
                                            "clock_ghz": round(ghz, 4), "mfma_busy": round(busy, 4),
                                            "frac_from_counters": round(frac, 4),
                                            **{n: c.get(n, 0) for n in UTIL_COUNTERS}}
-        md += ["", "Per dispatch of the counter pass: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the cycles "
-                   "the shader engines had waves (SQ_BUSY_CYCLES / engines); clock ≥ those cycles over the dispatch's "
+        md += ["", "Per dispatch of the counter pass: active cycles = SQ_BUSY_CYCLES / engines (the cycles the "
+                   "shader engines had waves); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES per SIMD over those cycles; "
+                   "clock ≥ those cycles over the dispatch's "
                    "duration; fraction of peak = MFMA cycles per SIMD over duration × 2.4 GHz (— for a dispatch under "
                    "20 us); VGPR as rocprofv3 records it (4 registers per granule where gfx950 wave64 allocates 8: "
                    "128 shown = 256 allocated).", "",

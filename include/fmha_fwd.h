@@ -134,17 +134,28 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
  *   FMHA_VARIANT_SHORT    the short entries: the regular grid at four blocks
  *                         per compute unit, K and V streamed through
  *                         two-stage LDS rings, any number of keys
+ *   FMHA_VARIANT_PAIR_STREAM  not varlen: pair blocks (FMHA_SPLIT_KBLOCK
+ *                         threads, 96 KiB of LDS) that each loop over
+ *                         M-tile pairs, the next pair's first K/V tiles and
+ *                         Q rows fetched during the current pair's last
+ *                         iterations and its O stored beside the next
+ *                         pair's first; dense: one block per compute unit
+ *                         taking every CU-count-th pair; causal: one block
+ *                         per pair of the first half of each (batch, head),
+ *                         taking that pair's mirror next
  * All forms give the same results up to fp32 rounding order.  Causal dense
  * launches of more than one batch whose K/V per XCD, batch x ceil(nhead_k/8)
  * x seqlen_k x 256 bytes, is at most 8 MiB run the form's tile-major entry
  * (every batch's heaviest M-tiles first), and causal varlen launches of at
- * most 64 sequences in the regular form a compact entry (the live M-tiles of
- * all sequences, highest M-tile index first), unless one order flag is OR-ed
- * into `variant`: FMHA_VARIANT_REFERENCE_ORDER (the reference's order),
- * FMHA_VARIANT_TILE_MAJOR_ORDER (tile-major / level order wherever it
- * exists) or FMHA_VARIANT_SEQUENCE_ORDER (varlen: longest sequence first);
- * the order changes no result bit.  An unknown variant, or more than one
- * order flag, returns hipErrorInvalidValue. */
+ * most 8 sequences in the regular form whose grid is at most 8 rounds of two
+ * blocks per compute unit the compact entry in the sequence order (longest
+ * sequence first, no block past a sequence's end between live ones), unless
+ * one order flag is OR-ed into `variant`: FMHA_VARIANT_REFERENCE_ORDER (the
+ * reference's order), FMHA_VARIANT_TILE_MAJOR_ORDER (tile-major, or for
+ * varlen the level order: the live M-tiles of all sequences, highest M-tile
+ * index first; at most 64 sequences) or FMHA_VARIANT_SEQUENCE_ORDER (varlen,
+ * at most 64 sequences); the order changes no result bit.  An unknown
+ * variant, or more than one order flag, returns hipErrorInvalidValue. */
 #define FMHA_VARIANT_AUTO 0
 #define FMHA_VARIANT_REGULAR 1
 #define FMHA_VARIANT_SPLITKV 2
@@ -153,6 +164,8 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_BALANCED 5 /* fmha_fwd_d64_bf16_ws only: it needs a workspace */
 #define FMHA_VARIANT_SHORT 6
 #define FMHA_VARIANT_BALANCED_PAIR 7 /* fmha_fwd_d64_bf16_ws only: the balanced form over M-tile pairs */
+#define FMHA_VARIANT_PAIR_STREAM 8   /* dense layouts (not varlen): one pair block per compute unit looping
+                                        over M-tile pairs (causal: a pair, then its mirror) */
 #define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
 #define FMHA_VARIANT_TILE_MAJOR_ORDER 32 /* flag: causal dense batches on the tile-major entries (any K/V
                                             size); causal varlen (regular form, <= 64 sequences): level order */

@@ -112,7 +112,8 @@ def check_problem(prob, dist="ref", seed=42, mult=1.0, rule="reference", variant
 # fails.  Every other configuration passes the plain rule outright.
 CONTRACT_BOUNDS = {
     "cfg5": {"auto": (15, 0.0059), "regular": (15, 0.0059), "pair": (15, 0.0059), "splitkv": (14, 0.0030),
-             "balanced": (15, 0.0059), "balanced_pair": (16, 0.0059), "short": (3, 0.0011)},
+             "balanced": (15, 0.0059), "balanced_pair": (16, 0.0059), "short": (3, 0.0011),
+             "pair_stream": (15, 0.0059)},
 }
 
 

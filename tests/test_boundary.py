@@ -194,11 +194,11 @@ def test_variant_validation():
     """An unknown kernel form is rejected before anything is launched."""
     lib = fmha.load_library()
     p = valid_params()
-    # 0-3 and 6 are the valid forms, optionally OR-ed with one order flag
+    # 0-3, 6 and 8 are the valid forms, optionally OR-ed with one order flag
     # (VARIANT_REFERENCE_ORDER 16, VARIANT_TILE_MAJOR_ORDER 32, VARIANT_SEQUENCE_ORDER 64); 4 is retired,
     # 5 and 7 (the balanced forms) need the workspace entry; two order flags at once are rejected
     R, T, S = fmha.VARIANT_REFERENCE_ORDER, fmha.VARIANT_TILE_MAJOR_ORDER, fmha.VARIANT_SEQUENCE_ORDER
-    for bad in (-1, 4, 5, 7, 8, 100, 128, R | 7, T | 4, R | T, T | S, R | S, R | T | S, R | T | 1):
+    for bad in (-1, 4, 5, 7, 9, 100, 128, R | 7, T | 4, R | T, T | S, R | S, R | T | S, R | T | 1):
         assert lib.fmha_fwd_d64_bf16_variant(ctypes.byref(p), 1, 0, bad, None) == INVALID, bad
     for bad in (R | T, T | S | 2):
         assert lib.fmha_fwd_d64_bf16_ws(ctypes.byref(p), 1, 1, bad, None, 0, None) == INVALID, bad
@@ -298,18 +298,19 @@ def test_auto_form_rule(batch, heads, seqlen, causal, cus, form):
     (17, 16, 2, 2048, 1, False, 0),    # 8.5 MiB
     (1, 16, 16, 8192, 1, False, 0),    # one batch: nothing to interleave
     (8, 16, 16, 1024, 0, False, 0),    # dense: every block costs the same
-    (8, 16, 16, 1024, 1, True, 1),     # varlen causal: the compact order (regular form, <= 64 sequences)
-    (64, 16, 16, 1024, 1, True, 1),
-    (65, 16, 16, 1024, 1, True, 0),    # more sequences than lanes: the reference's order
+    (8, 16, 16, 1024, 1, True, 2),     # varlen causal, <= 8 sequences, grid 1024 <= 16 x 256: sequence order
+    (8, 16, 16, 4096, 1, True, 2),     # grid 4096 = 16 x 256 (cfg4's bound is 3968)
+    (8, 16, 16, 4224, 1, True, 0),     # grid 4224 > 16 x 256: the reference's order
+    (9, 16, 16, 1024, 1, True, 0),     # more than 8 sequences: the reference's order
     (8, 16, 16, 1024, 0, True, 0),     # varlen dense: the reference's order
     (1, 8, 8, 4096, 1, True, 0),       # the split-KV form keeps the reference's order
-    (64, 16, 16, 128, 1, True, 0),     # so does the short form
+    (8, 64, 64, 128, 1, True, 0),      # so does the short form
 ])
 def test_tile_major_rule(batch, heads, kv_heads, seqlen, causal, varlen, expect):
     """Causal dense batches run tile-major while the K/V one XCD serves,
-    batch x ceil(nhead_k/8) x seqlen_k x 256 bytes, is at most 8 MiB; causal
-    varlen launches of at most 64 sequences in the regular form run the
-    compact order."""
+    batch x ceil(nhead_k/8) x seqlen_k x 256 bytes, is at most 8 MiB (1);
+    causal varlen launches in the regular form of at most 8 sequences on a
+    grid of at most 16 x CUs blocks run the sequence order (2)."""
     p = valid_params(lse=False)
     p.nhead_q, p.nhead_k = heads, kv_heads
     p.seqlen_q = p.seqlen_k = seqlen

@@ -49,7 +49,9 @@ def test_every_entry_compiled(asm):
     for e in _ENTRIES:
         assert any(e + "13FmhaFwdParams" in n for n in names), e
     for e in ("fmha_fwd_d64_bf16_balanced_msk1", "fmha_fwd_d64_bf16_balanced_pair_msk1",
-              "fmha_fwd_d64_bf16_balanced_merge"):
+              "fmha_fwd_d64_bf16_balanced_merge", "fmha_fwd_d64_bf16_pair_stream_msk0",
+              "fmha_fwd_d64_bf16_pair_stream_msk1", "fmha_fwd_d64_bf16_msk1_varlen_tilemajor",
+              "fmha_fwd_d64_bf16_msk1_varlen_seqmajor"):
         assert any(e in n for n in names), e
     for m in (0, 1):
         for v in ("", "_varlen"):

@@ -37,9 +37,12 @@ def _report(res):
 
 
 # every kernel form behind the launcher without a workspace: the
-# reference-named entries, the split-KV entries and the pair entries (the
-# automatic choice is one of them or the short form)
-FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR}
+# reference-named entries, the split-KV entries, the pair entries and the
+# pair stream entries (the automatic choice is one of them or the short
+# form); the pair stream form takes dense layouts only (the launcher rejects
+# varlen for it)
+FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR,
+         "pair_stream": fmha.VARIANT_PAIR_STREAM}
 # the balanced form (causal dense, through the workspace entry) runs on the
 # matrices of reference cases and benchmark configurations
 MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, balanced_pair=fmha.VARIANT_BALANCED_PAIR,
@@ -47,6 +50,8 @@ MATRIX_FORMS = dict(FORMS, balanced=fmha.VARIANT_BALANCED, balanced_pair=fmha.VA
 
 
 def _dense_only(form, prob):
+    if form == "pair_stream" and prob.varlen:
+        pytest.skip("the pair stream form takes dense layouts only")
     if form.startswith("balanced") and (prob.varlen or not prob.causal):
         pytest.skip("the balanced forms take causal dense problems only")
 
@@ -156,6 +161,8 @@ def test_gqa_equals_replicated_mha_bitwise(form):
 
 @pytest.mark.parametrize("form", list(FORMS))
 def test_varlen_equals_per_sequence_dense_bitwise(form):
+    if form == "pair_stream":
+        pytest.skip("the pair stream form takes dense layouts only")
     seqs = (1, 77, 128, 300, 64, 513)
     pv = Problem(batch=0, nhead_q=4, nhead_k=2, seqlen_q=0, causal=True, lse=True, varlen_seqs=seqs)
     q, k, v = make_inputs(pv, "normal", 5)
@@ -244,7 +251,7 @@ def test_compact_varlen_orders_equal_reference_order_bitwise(seqs, heads, kv_hea
     seq = torch.from_numpy(p.seqstart())
     prm = build_params(p, *host, torch.empty(nlse, dtype=torch.float32), seq)
     regular = fmha.pick_variant(prm, p.batch, 1) == fmha.VARIANT_REGULAR
-    assert (fmha.tile_major(prm, p.batch, 1) != 0) == regular
+    assert fmha.tile_major(prm, p.batch, 1) in ((0, 2) if regular and p.batch <= 8 else (0,))
     q, k, v = make_inputs(p, "normal", 37)
     o_r, l_r = run_kernel(p, q, k, v, variant=fmha.VARIANT_REGULAR | fmha.VARIANT_REFERENCE_ORDER)
     o_ora, l_ora = oracle.run(p, q, k, v)
@@ -263,6 +270,8 @@ def test_masked_and_foreign_keys_contribute_nothing(form):
     wrongly included key would get a sizeable weight; V = 16384.0); the
     row's output bits must not change.  (1) the other sequences of a packed varlen batch, (2) the
     causally masked future key."""
+    if form == "pair_stream":
+        pytest.skip("the pair stream form takes dense layouts only")
     seqs = (190, 64, 333)
     T = sum(seqs)
     s0 = seqs[0]
@@ -481,6 +490,47 @@ def test_padded_strides_match_dense(form):
     assert np.array_equal(dl.cpu().numpy(), l_dense)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("batch,heads,kv_heads,seqlen_q,seqlen_k", [
+    (4, 16, 16, 2048, 2048),   # two rounds of 256 pair blocks (cfg2's shape)
+    (1, 16, 16, 8192, 8192),   # cfg3's shape
+    (3, 5, 1, 700, 900),       # odd M-tile count: the last pair's second M-tile is past the rows
+    (2, 8, 4, 1000, 333),      # Sq > Sk: causal rows with no visible key
+    (1, 3, 3, 4100, 4100),     # fewer pairs than compute units; a causal odd pair count (the middle pair alone)
+    (5, 16, 8, 1536, 1536),    # 480 pairs: a partial second round
+])
+def test_pair_stream_equals_pair_bitwise(batch, heads, kv_heads, seqlen_q, seqlen_k, causal):
+    """The pair stream form computes every pair with the pair form's
+    arithmetic (the same tile order, frame and epilogue; its padding tiles
+    and the causal tiles the pair form skips add exact zeros), so O and LSE
+    match the pair form bit for bit, and every row is written (O starts as a
+    NaN pattern)."""
+    p = Problem(batch=batch, nhead_q=heads, nhead_k=kv_heads, seqlen_q=seqlen_q, seqlen_k=seqlen_k, causal=causal,
+                lse=True)
+    q, k, v = make_inputs(p, "normal", 53)
+    o_s, l_s = run_kernel(p, q, k, v, variant=fmha.VARIANT_PAIR_STREAM)
+    o_p, l_p = run_kernel(p, q, k, v, variant=fmha.VARIANT_PAIR | fmha.VARIANT_REFERENCE_ORDER)
+    print("pair stream vs pair", (batch, heads, kv_heads, seqlen_q, seqlen_k, causal), flush=True)
+    assert np.array_equal(o_s, o_p)
+    assert np.array_equal(l_s, l_p)
+
+
+def test_pair_stream_rejects_varlen():
+    """The pair stream form is for dense layouts: a varlen launch asking for
+    it is refused before anything runs."""
+    import torch
+
+    from harness import build_params
+
+    p = Problem(batch=0, nhead_q=2, seqlen_q=0, varlen_seqs=(100, 200))
+    nq, nk, nlse = p.sizes()
+    t = [torch.zeros(n, dtype=torch.int16, device="cuda:0") for n in (nq, nk, nk, nq)]
+    seq = torch.from_numpy(p.seqstart()).to("cuda:0")
+    prm = build_params(p, *t, None, seq)
+    with pytest.raises(fmha.FmhaError):
+        fmha.fmha_fwd_d64_bf16(prm, p.batch, 0, None, fmha.VARIANT_PAIR_STREAM)
+
+
 def test_retired_variant_rejected():
     """Variant value 4 (a queue-based persistent form, removed) is refused
     before anything runs, as any unknown variant."""
@@ -492,7 +542,7 @@ def test_retired_variant_rejected():
     nq, nk, nlse = p.sizes()
     t = [torch.zeros(n, dtype=torch.int16, device="cuda:0") for n in (nq, nk, nk, nq)]
     prm = build_params(p, *t, None, None)
-    for v in (4, 8, -1):
+    for v in (4, 9, -1):
         with pytest.raises(fmha.FmhaError):
             fmha.fmha_fwd_d64_bf16(prm, p.batch, 0, None, v)
 

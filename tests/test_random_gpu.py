@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 N_CASES = 40
 FORMS = {"regular": fmha.VARIANT_REGULAR, "splitkv": fmha.VARIANT_SPLITKV, "pair": fmha.VARIANT_PAIR,
-         "short": fmha.VARIANT_SHORT}
+         "short": fmha.VARIANT_SHORT, "pair_stream": fmha.VARIANT_PAIR_STREAM}
 
 
 def _draw(i):
@@ -57,6 +57,8 @@ def _need_gpu():
 @pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("prob", CASES, ids=[c.name for c in CASES])
 def test_random_shape_matches_oracle(prob, form):
+    if form == "pair_stream" and prob.varlen:
+        pytest.skip("the pair stream form takes dense layouts only")
     res = check_problem(prob, dist="ref", seed=7, rule="reference", variant=FORMS[form])
     print(res, flush=True)
     assert res["pass"], res
@@ -98,7 +100,8 @@ def test_wide_random_sweep():
         q, k, v = make_inputs(prob, "ref", 100 + i)
         o_ref, lse_ref = oracle.run(prob, q, k, v)
         for name, var in forms.items():
-            if name.startswith("balanced") and (prob.varlen or not prob.causal):
+            if (name.startswith("balanced") and (prob.varlen or not prob.causal)) or \
+                    (name == "pair_stream" and prob.varlen):
                 continue
             ob, lb = run_kernel(prob, q, k, v, variant=var)
             ok = verify.reference_rule(o_ref, verify.bf16_bits_to_f32(ob))["pass"]
