@@ -122,6 +122,8 @@ __device__ __forceinline__ void vmcnt_wait() {
 // s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and
 // [15:14], expcnt [6:4] and lgkmcnt [11:8] at their no-wait maxima)
 constexpr int kWaitVmcnt0 = 0x0F70;
+// s_waitcnt immediate for lgkmcnt(0) alone (vmcnt and expcnt at their maxima)
+constexpr int kWaitLgkmcnt0 = 0xC07F;
 // Workgroup barrier of the K/V ring, without __syncthreads()'s memory fence:
 // that fence waits vmcnt(0), i.e. also for the prefetches still in flight.
 // Before the barrier each wave has waited for its own DMA of the tile about
@@ -1211,6 +1213,9 @@ __device__ __forceinline__ void fwd_pair_stream(const Ring& ring, lds_char* qbuf
         const int t = X.npad - kRing;
         const bool has_next = KX + 1 < n_mine;
         const StreamKV N = stream_kv<kCausal>(sargs_here(), KX + 1, has_next);
+        // the kernarg reads above retired where the compiler's wait placement
+        // sees it (see `settled`)
+        __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
         iteration(t, P0{}, N, 0, X, t + 2, W4{}, NoQ{});
         iteration(t + 1, P1{}, N, 1, X, t + 3, W4{}, NoQ{});
         iteration(t + 2, P2{}, N, 2, N, 0, W4{}, NoQ{});
@@ -1261,8 +1266,19 @@ __device__ __forceinline__ void fwd_pair_stream(const Ring& ring, lds_char* qbuf
     ring_barrier();
     asm volatile("" ::"v"(qop[0]), "v"(qop[1]), "v"(qop[2]), "v"(qop[3]));
     gemm0(P0{}, sacc[0]);
+    // Scalar loads (the kernarg reads of an item) and LDS reads share lgkmcnt,
+    // and scalar loads return out of order: while one may be in flight the
+    // compiler can only wait for an LDS operand with lgkmcnt(0), which also
+    // waits for the reads issued ahead for the next MFMAs.  The ring
+    // barrier's own lgkmcnt(0) is inline asm, which the compiler does not
+    // see, so every item's kernarg reads are retired with the builtin before
+    // the iterations: otherwise the loop header, reached with them possibly
+    // in flight, puts lgkmcnt(0) before every operand of every fourth
+    // iteration (2-3 % per tile).
+    auto settled = [&]() { __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0); };
     bool prev = false;
     while (true) {
+        settled();
         if (prev)
             first(std::true_type{});
         else
@@ -1273,11 +1289,23 @@ __device__ __forceinline__ void fwd_pair_stream(const Ring& ring, lds_char* qbuf
         iteration(1, P1{}, X, 1 + kRing, X, 1 + 2, W4{}, std::true_type{});
         iteration(2, P2{}, X, 2 + kRing, X, 2 + 2, W8{}, NoQ{});
         iteration(3, P3{}, X, 3 + kRing, X, 3 + 2, W8{}, NoQ{});
-        for (int t = kRing; t < X.npad - kRing; t += kRing) {
-            mid(t, P0{});
-            mid(t + 1, P1{});
-            mid(t + 2, P2{});
-            mid(t + 3, P3{});
+        settled();
+        // iterations 4 .. npad-5 (none when npad = 8): the unrolled loop
+        // starts at phase 1 like the other forms' loops, whose compiled code
+        // keeps two LDS operand reads in flight in every phase (starting at
+        // phase 0 the compiler stages that phase's V operands through one
+        // register set and waits for each read)
+        if (X.npad > 2 * kRing) {
+            mid(kRing, P0{});
+            for (int t = kRing + 1; t + kRing <= X.npad - 2 * kRing + 1; t += kRing) {  // t .. t+3 <= npad-8
+                mid(t, P1{});
+                mid(t + 1, P2{});
+                mid(t + 2, P3{});
+                mid(t + 3, P0{});
+            }
+            mid(X.npad - 2 * kRing + 1, P1{});
+            mid(X.npad - 2 * kRing + 2, P2{});
+            mid(X.npad - 2 * kRing + 3, P3{});
         }
         if (!tail()) break;
         smz = sm;
