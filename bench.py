@@ -423,7 +423,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
     ap.add_argument("--only", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
                     help="time one workload only (profiling runs)")
-    ap.add_argument("--variant", default="auto", help="with --only: the kernel form (default: the launcher's choice)")
+    ap.add_argument("--variant", default="auto", help="with --only: the kernel form, optionally |reference, |tilemajor or |sequence "
+                         "(default: the launcher's choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run `steps` device-to-device copies of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -453,7 +454,7 @@ def main():
         from fmha_native_amd.problem import baseline_problems
 
         prob, mult = {"cfg2": (cfg2, 1.0), "cfg3": (cfg3, 1.0)}.get(args.only) or baseline_problems()[args.only]
-        r = time_problem(prob, args.steps, args.warmup, torch, mult, fmha.VARIANTS[args.variant])
+        r = time_problem(prob, args.steps, args.warmup, torch, mult, fmha.variant_code(args.variant))
         # launch order, for a profiler's trace: ramp, warmup, steps timed back
         # to back, then as many under the reference's protocol
         print(json.dumps({"workload": args.only, "ms_per_step": r["ms"], "tflops": r["tflops"], "form": r["form"],

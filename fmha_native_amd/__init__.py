@@ -29,6 +29,7 @@ __all__ = [
     "LOG2E", "HIP_ERROR_INVALID_VALUE", "VARIANT_AUTO", "VARIANT_REGULAR", "VARIANT_SPLITKV", "VARIANT_PAIR",
     "VARIANT_BALANCED", "VARIANT_SHORT", "VARIANT_BALANCED_PAIR", "VARIANT_PAIR_STREAM", "fmha_fwd_d64_bf16_ws", "workspace_size", "balanced_plan",
     "VARIANT_REFERENCE_ORDER", "VARIANT_TILE_MAJOR_ORDER", "VARIANT_SEQUENCE_ORDER", "VARIANTS",
+    "ORDERS", "variant_code",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -133,6 +134,20 @@ VARIANT_SEQUENCE_ORDER = 64
 VARIANTS = {"auto": VARIANT_AUTO, "regular": VARIANT_REGULAR, "splitkv": VARIANT_SPLITKV, "pair": VARIANT_PAIR,
             "balanced": VARIANT_BALANCED, "short": VARIANT_SHORT,
             "balanced_pair": VARIANT_BALANCED_PAIR, "pair_stream": VARIANT_PAIR_STREAM}
+ORDERS = {"reference": VARIANT_REFERENCE_ORDER, "tilemajor": VARIANT_TILE_MAJOR_ORDER,
+          "sequence": VARIANT_SEQUENCE_ORDER}
+
+
+def variant_code(v):
+    """Launcher code of a variant name: a form of ``VARIANTS`` optionally
+    followed by ``|reference``, ``|tilemajor`` or ``|sequence`` (one block-order
+    flag), e.g. ``"regular|sequence"``; an integer or digit string is taken
+    as the code itself."""
+    if isinstance(v, int):
+        return v
+    name, _, order = str(v).partition("|")
+    code = int(name) if name.isdigit() else VARIANTS[name]
+    return code | (ORDERS[order] if order else 0)
 
 
 def fmha_fwd_d64_bf16(params, batch, causal, stream=None, variant=VARIANT_AUTO):

@@ -52,6 +52,7 @@ import argparse
 import glob
 import json
 import os
+import shlex
 import sqlite3
 import subprocess
 import sys
@@ -89,7 +90,7 @@ def _run(name, prof_args, prog, out_dir, limit):
     lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
     if not dbs or not lines:
         raise RuntimeError(f"pass {name} failed (rc={r.returncode}); see {name}.log")
-    shown = " ".join("python3" if c == sys.executable else c for c in cmd[4:]).replace(ROOT + "/", "")
+    shown = " ".join("python3" if c == sys.executable else shlex.quote(c) for c in cmd[4:]).replace(ROOT + "/", "")
     return dbs[0], json.loads(lines[-1]), shown
 
 
@@ -186,12 +187,12 @@ def profile_forms(args):
 
     probs = baseline_problems()
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on " + ", ".join(args.forms.split(",")), "",
-          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof --forms "
-          f"{args.forms}` on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
+          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof "
+          f"{' '.join(shlex.quote(a) for a in sys.argv[1:])}` on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
           "`auto` is the launcher's own choice. TFLOP/s use the repo FLOP convention "
           "(4·B·H·Sq·Sk·64, ×0.5 causal; varlen counts max(S) for every sequence, and the exact count of "
           "visible (q, k) pairs is given beside it).", ""]
-    fig = {"made_by": f"python -m fmha_native_amd.rocprof --forms {args.forms}", "forms": {}}
+    fig = {"made_by": f"python -m fmha_native_amd.rocprof --forms {shlex.quote(args.forms)}", "forms": {}}
     # the counters' scale, from a device copy of known size (as the main run)
     copy = {}
     copy_cmds = []
@@ -206,7 +207,7 @@ def profile_forms(args):
     for spec in args.forms.split(","):
         wl, form = spec.split(":")
         prob, _mult = probs[wl]
-        tag = f"{wl}_{form}"
+        tag = f"{wl}_{form}".replace("|", "-")
         steps = str(args.steps // 4 if wl != "cfg1" else args.steps)
         # unprofiled
         cmd = _bench("--only", wl, "--variant", form, "--steps", steps, "--warmup", "5")
@@ -278,7 +279,7 @@ def profile_forms(args):
                    f"{t.get('WRITE_SIZE', 0) / 1e6:.1f} MB" for k, t in sorted(traffic.items()))
                + f"; total {hbm / 1e6:.1f} MB against {alg / 1e6:.1f} MB algorithmic ({hbm / alg:.2f}x).", "",
                "Commands:", "",
-               f"    python3 bench.py --only {wl} --variant {form} --steps {steps} --warmup 5",
+               f"    python3 bench.py --only {wl} --variant {shlex.quote(form)} --steps {steps} --warmup 5",
                f"    {tcmd}", f"    {ucmd}"] + [f"    {c}" for c in tcmds] + [""]
         entry["traffic"] = {"hbm_bytes": int(hbm), "algorithmic_bytes": int(alg),
                             "kernels": {k: {c: int(v) for c, v in t.items()} for k, t in traffic.items()}}

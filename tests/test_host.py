@@ -241,3 +241,33 @@ def test_merge_partials_rejects(case, match):
         kw["lse"] = torch.zeros(11, dtype=torch.float32)
     with pytest.raises(ValueError, match=match):
         fmha.merge_partials(o_parts, lse_parts, **kw)
+
+
+def test_abtest_variants_and_specs():
+    """The A/B tool's variant names resolve to the launcher's codes (a form,
+    optionally with one block-order flag), and every committed spec names
+    known forms and valid problems."""
+    import glob
+    import os
+    import json
+
+    from fmha_native_amd import abtest
+    from fmha_native_amd.problem import Problem
+
+    assert abtest.parse_variant("pair") == fmha.VARIANT_PAIR
+    assert abtest.parse_variant("regular|reference") == fmha.VARIANT_REGULAR | fmha.VARIANT_REFERENCE_ORDER
+    assert abtest.parse_variant("regular|tilemajor") == fmha.VARIANT_REGULAR | fmha.VARIANT_TILE_MAJOR_ORDER
+    assert abtest.parse_variant("regular|sequence") == fmha.VARIANT_REGULAR | fmha.VARIANT_SEQUENCE_ORDER
+    assert abtest.parse_variant("pair_stream") == fmha.VARIANT_PAIR_STREAM
+    assert abtest.parse_variant(3) == 3
+    specs = glob.glob(os.path.join(os.path.dirname(fmha.__file__), "abspecs", "*.json"))
+    assert specs
+    for path in specs:
+        with open(path) as f:
+            for case in json.load(f):
+                kw = dict(case["problem"])
+                if "varlen_seqs" in kw:
+                    kw["varlen_seqs"] = tuple(kw["varlen_seqs"])
+                Problem(**kw)
+                for v in case["variants"]:
+                    abtest.parse_variant(v)
