@@ -196,8 +196,10 @@ def time_problem(prob, steps, warmup, torch, mult=1.0, variant=0):
     torch.cuda.synchronize()
     ref_ms = sum(times) / steps
     hip.destroy([e0, e1])
-    picked = variant or fmha.pick_variant(p, batch, causal)
-    form = ("balanced pair" if variant == fmha.VARIANT_BALANCED_PAIR else "balanced") + \
+    orders = fmha.VARIANT_REFERENCE_ORDER | fmha.VARIANT_TILE_MAJOR_ORDER | fmha.VARIANT_SEQUENCE_ORDER
+    picked = (variant & ~orders) or fmha.pick_variant(p, batch, causal)
+    plain = ", plain heaviest-first table" if variant & fmha.VARIANT_REFERENCE_ORDER else ""
+    form = ("balanced pair" if picked == fmha.VARIANT_BALANCED_PAIR else "balanced") + plain + \
         " (two launches: items, then the merge of split M-tiles)" if need > 0 else \
         {v: k for k, v in fmha.VARIANTS.items()}.get(picked, "?")
     return {"ms": ms, "wall_ms": wall * 1e3 / steps, "tflops": prob.flops() / (ms * 1e-3) / 1e12, "ramp": ramp,

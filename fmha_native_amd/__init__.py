@@ -99,7 +99,7 @@ def load_library(path=LIB_PATH):
     lib.fmha_fwd_d64_bf16_workspace_size.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.fmha_fwd_d64_bf16_workspace_size.restype = ctypes.c_int64
     lib.fmha_fwd_d64_bf16_balanced_plan.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                                    ctypes.POINTER(ctypes.c_uint16), ctypes.c_int,
+                                                    ctypes.c_int, ctypes.POINTER(ctypes.c_uint16), ctypes.c_int,
                                                     ctypes.POINTER(ctypes.c_int)]
     lib.fmha_fwd_d64_bf16_balanced_plan.restype = ctypes.c_int
     ip = ctypes.POINTER(ctypes.c_int)
@@ -188,19 +188,22 @@ def workspace_size(params, batch, causal, variant=VARIANT_AUTO):
                                                            int(variant))
 
 
-def balanced_plan(params, batch, causal, compute_units=0, force=False):
+def balanced_plan(params, batch, causal, compute_units=0, force=False, xccs=0):
     """(items, split_from) of the balanced form's plan: items per (batch,
     head) in dispatch order as (unit, half) pairs, half None for a whole
     unit; ([], None) when the launch would not be balanced.  ``force``: False
     (the automatic rule), True (over M-tiles, as VARIANT_BALANCED) or "pair"
     (over M-tile pairs, as VARIANT_BALANCED_PAIR: unit u is M-tiles 2u and
-    2u+1).  split_from counts M-tiles.  Host only."""
+    2u+1).  ``xccs``: XCD count of the dispatch order (0: the current
+    device's, 8 without one; 1: plain heaviest first, as launched with
+    VARIANT_REFERENCE_ORDER).  split_from counts M-tiles.  Host only."""
     pair = force == "pair"
     cap = 4096
     buf = (ctypes.c_uint16 * cap)()
     sf = ctypes.c_int(-1)
     n = load_library().fmha_fwd_d64_bf16_balanced_plan(ctypes.byref(params), int(batch), int(causal),
-                                                       int(compute_units), 2 if pair else int(bool(force)), buf, cap,
+                                                       int(compute_units), int(xccs), 2 if pair else int(bool(force)),
+                                                       buf, cap,
                                                        ctypes.byref(sf))
     if n < 0:
         raise FmhaError(HIP_ERROR_INVALID_VALUE, "fmha_fwd_d64_bf16_balanced_plan")

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 
 #include "fmha_fwd.h"
 #include "fmha_internal.h"
@@ -262,30 +263,30 @@ int causal_ntiles(const FmhaFwdParams* p, int mt) {
 // Modes: the automatic rule, or forced over single M-tiles
 // (FMHA_VARIANT_BALANCED) or over M-tile pairs (FMHA_VARIANT_BALANCED_PAIR).
 enum PlanMode : int { kPlanAuto = 0, kPlanSingle = 1, kPlanPair = 2 };
-bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode,
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int xccs, int mode,
                          FmhaBalancedArgs* a, int64_t* ws_bytes);
 
 // The plan depends on the launch's shape only, so the last one built on a
 // thread is kept: a serving loop relaunching one shape skips the sort (about
 // 10 us of host time for cfg5's 531 items).
-bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode, FmhaBalancedArgs* a,
-                   int64_t* ws_bytes) {
+bool balanced_plan(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int xccs, int mode,
+                   FmhaBalancedArgs* a, int64_t* ws_bytes) {
     struct Key {
-        int seqlen_q, seqlen_k, nhead_q, batch, causal, varlen, mode;
+        int seqlen_q, seqlen_k, nhead_q, batch, causal, varlen, mode, xccs;
         int64_t cus;
         bool operator==(const Key& o) const {
             return seqlen_q == o.seqlen_q && seqlen_k == o.seqlen_k && nhead_q == o.nhead_q && batch == o.batch &&
-                   causal == o.causal && varlen == o.varlen && mode == o.mode && cus == o.cus;
+                   causal == o.causal && varlen == o.varlen && mode == o.mode && xccs == o.xccs && cus == o.cus;
         }
     };
-    thread_local Key last_key{-1, -1, -1, -1, -1, -1, -1, -1};
+    thread_local Key last_key{-1, -1, -1, -1, -1, -1, -1, -1, -1};
     thread_local bool last_ok = false;
     thread_local int64_t last_bytes = 0;
     thread_local FmhaBalancedArgs last_plan;
     const Key key{p->seqlen_q, p->seqlen_k, p->nhead_q, batch, causal, p->seqstart_q != nullptr ? 1 : 0,
-                  mode, cus};
+                  mode, xccs, cus};
     if (!(key == last_key)) {
-        last_ok = balanced_plan_build(p, batch, causal, cus, mode, &last_plan, &last_bytes);
+        last_ok = balanced_plan_build(p, batch, causal, cus, xccs, mode, &last_plan, &last_bytes);
         last_key = key;
     }
     if (!last_ok) return false;
@@ -325,7 +326,37 @@ bool balanced_pays(int64_t blocks, int heaviest, double avg, int64_t cus) {
     return heaviest >= 128 && heaviest > 1.5 * avg;
 }
 
-bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int mode,
+// Dispatch order of a plan's items (sorted heaviest first) that lets each
+// XCD's L2 serve items reading the same keys.  Workgroup i of a launch runs
+// on XCD i % xccs, and table entry z is block (h, b, z) of every (batch,
+// head), linear id h + nhead_q * (b + batch * z); when hb = nhead_q * batch
+// divides xccs into g = xccs / hb >= 2 groups, entry z runs on the XCDs of
+// group z % g only.  Blocks are dispatched in order, one group after the
+// other, so every run of g consecutive entries (one per group) must keep
+// items of about equal work, or a group with busy slots holds back the
+// dispatch of the others (a list schedule that gave each group its own run
+// of heaviest items measured 20-29 % slower on B1 H1 S40000 and B1 H2
+// S16384).  Within each such run the items are therefore only re-ordered by
+// the first key tile they read (first halves and whole M-tiles, which start
+// at key 0, to the lower groups; second halves, which start half-way, to the
+// higher ones), so each group keeps taking items that start at the same key.
+// Otherwise (hb not a divisor of xccs, or xccs <= 1) the order stays
+// heaviest first.  Allocates nothing.
+template <class Start>
+void xcd_order(int n, int xccs, int64_t hb, Start start, int* order) {
+    for (int i = 0; i < n; ++i) order[i] = i;
+    if (xccs <= 1 || hb >= xccs || xccs % hb != 0) return;
+    const int g = (int)(xccs / hb);
+    for (int r = 0; r < n; r += g) {
+        const int e = std::min(n, r + g);
+        std::sort(order + r, order + e, [&](int x, int y) {
+            const int sx = start(x), sy = start(y);
+            return sx != sy ? sx < sy : x < y;
+        });
+    }
+}
+
+bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t cus, int xccs, int mode,
                          FmhaBalancedArgs* a, int64_t* ws_bytes) {
     if (!causal || p->seqstart_q != nullptr || batch <= 0 || p->seqlen_q <= 0 || cus <= 0) return false;
     const int m_tiles = (p->seqlen_q + kM0 - 1) / kM0;
@@ -383,7 +414,12 @@ bool balanced_plan_build(const FmhaFwdParams* p, int batch, int causal, int64_t 
             if (x.u != y.u) return x.u > y.u;
             return x.half < y.half;
         });
-        for (int i = 0; i < n_items; ++i) a->item[i] = (unsigned short)(items[i].u | (items[i].half << 15));
+        // the first key tile an item reads (a second half starts past the first)
+        int order[FMHA_BALANCED_MAX_ITEMS];
+        xcd_order(n, xccs, (int64_t)p->nhead_q * batch,
+                  [&](int i) { return items[i].half ? (work(items[i].u) + 1) / 2 : 0; }, order);
+        for (int i = 0; i < n_items; ++i)
+            a->item[i] = (unsigned short)(items[order[i]].u | (items[order[i]].half << 15));
         a->split_from = split_from;
         a->n_split = n_split;
         a->n_items = n_items;
@@ -403,11 +439,13 @@ int plan_mode(int v) {
 }  // namespace
 
 extern "C" int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* p, int batch, int causal, int compute_units,
-                                               int force, unsigned short* items, int capacity, int* split_from) {
-    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0) return -1;
+                                               int xccs, int force, unsigned short* items, int capacity,
+                                               int* split_from) {
+    if (fmha_fwd_d64_bf16_check(p, batch, causal) != hipSuccess || compute_units < 0 || xccs < 0) return -1;
     if (force < kPlanAuto || force > kPlanPair) return -1;
     FmhaBalancedArgs a;
-    if (!balanced_plan(p, batch, causal, compute_units > 0 ? compute_units : device_cus(), force, &a, nullptr))
+    if (!balanced_plan(p, batch, causal, compute_units > 0 ? compute_units : device_cus(),
+                       xccs > 0 ? xccs : device_shape().xccs, force, &a, nullptr))
         return 0;
     if (items != nullptr)
         for (int i = 0; i < a.n_items && i < capacity; ++i) items[i] = a.item[i];
@@ -421,7 +459,9 @@ extern "C" int64_t fmha_fwd_d64_bf16_workspace_size(const FmhaFwdParams* p, int 
     const int mode = plan_mode(variant & ~kOrderFlags);
     if (mode < 0) return 0;
     int64_t bytes = 0;
-    if (!balanced_plan(p, batch, causal, device_cus(), mode, nullptr, &bytes)) return 0;
+    // the same plan (and cache entry) as the launch with this variant
+    const int xccs = order_of(variant) == kOrderReference ? 1 : device_shape().xccs;
+    if (!balanced_plan(p, batch, causal, device_cus(), xccs, mode, nullptr, &bytes)) return 0;
     return bytes;
 }
 
@@ -438,7 +478,10 @@ extern "C" hipError_t fmha_fwd_d64_bf16_ws(const FmhaFwdParams* p, int batch, in
     if (batch == 0 || p->seqlen_q == 0) return hipSuccess;
     FmhaBalancedArgs a;
     int64_t need = 0;
-    const bool plan = balanced_plan(p, batch, causal, device_cus(), mode, &a, &need);
+    // the reference-order flag keeps the plain heaviest-first table (the
+    // results are the same bit for bit: the items do not change)
+    const int xccs = order_of(variant) == kOrderReference ? 1 : device_shape().xccs;
+    const bool plan = balanced_plan(p, batch, causal, device_cus(), xccs, mode, &a, &need);
     if (mode != kPlanAuto && (!plan || need > workspace_bytes)) return hipErrorInvalidValue;
     if (!plan || need > workspace_bytes) return fmha_fwd_d64_bf16_variant(p, batch, causal, variant, stream);
     a.p = *p;

@@ -227,15 +227,20 @@ hipError_t fmha_fwd_d64_bf16_noalloc(const FmhaFwdParams* params, int batch, int
                                      hipStream_t stream);
 
 /* The balanced form's plan for these arguments on a device with
- * `compute_units` compute units (0 = the current device's; `force` 0: the
- * automatic rule, 1: as FMHA_VARIANT_BALANCED, 2: as
+ * `compute_units` compute units and `xccs` XCDs (0 = the current device's;
+ * xccs 1 gives the plain heaviest-first order that FMHA_VARIANT_REFERENCE_ORDER
+ * launches; `force` 0: the automatic rule, 1: as FMHA_VARIANT_BALANCED, 2: as
  * FMHA_VARIANT_BALANCED_PAIR, whose items are M-tile pairs): writes up to
  * `capacity` items (dispatch order; M-tile (pair) | half << 15, half 0 = the
- * first ceil(n/2) key tiles) and the first split M-tile (even for pairs), and returns the number of items per (batch, head); 0 when
- * the launch would not be balanced, -1 for rejected arguments.  Host only
+ * first ceil(n/2) key tiles) and the first split M-tile (even for pairs), and
+ * returns the number of items per (batch, head); 0 when the launch would not
+ * be balanced, -1 for rejected arguments.  When nhead_q * batch divides xccs
+ * into g >= 2 groups of XCDs (entry z runs on group z % g), each run of g
+ * consecutive entries is ordered by the first key tile its items read, so
+ * that a group keeps taking items that start at the same key.  Host only
  * (this build's own; no counterpart in the reference). */
-int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* params, int batch, int causal, int compute_units, int force,
-                                    unsigned short* items, int capacity, int* split_from);
+int fmha_fwd_d64_bf16_balanced_plan(const FmhaFwdParams* params, int batch, int causal, int compute_units, int xccs,
+                                    int force, unsigned short* items, int capacity, int* split_from);
 
 /* Argument checks of fmha_fwd_d64_bf16 without launching (host only, no GPU
  * needed).  Returns hipSuccess or hipErrorInvalidValue. */

@@ -71,7 +71,8 @@ def run_kernel(prob, q, k, v, stream=None, variant=0):
     p = build_params(prob, dq, dk, dv, do, dlse, dseq)
     if stream is None:
         stream = torch.cuda.current_stream().cuda_stream
-    if variant in (fmha.VARIANT_BALANCED, fmha.VARIANT_BALANCED_PAIR):
+    orders = fmha.VARIANT_REFERENCE_ORDER | fmha.VARIANT_TILE_MAJOR_ORDER | fmha.VARIANT_SEQUENCE_ORDER
+    if variant & ~orders in (fmha.VARIANT_BALANCED, fmha.VARIANT_BALANCED_PAIR):
         # the balanced form runs through the workspace entry point
         need = fmha.workspace_size(p, prob.batch, int(prob.causal), variant)
         ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda:0")

@@ -115,6 +115,36 @@ def test_balanced_pair_equals_pair_and_splitkv_per_mtile(b, h, hk, sq, sk, lse, 
         assert verify.lse_rule(l_ref, lb)["pass"]
 
 
+@pytest.mark.parametrize("form", ["balanced", "balanced_pair"])
+@pytest.mark.parametrize("b,h,sq,mult", [
+    (1, 2, 40000, 2.0),   # the benchmark configuration: 4 XCD groups per (batch, head)
+    (1, 1, 20000, 1.0),   # 8 groups
+    (1, 4, 16384, 1.0),   # 2 groups
+    (2, 1, 12000, 1.0),   # 4 groups, two batches
+])
+def test_xcd_ordered_table_equals_plain_order_bitwise(form, b, h, sq, mult):
+    """The default table orders each run of XCD groups by first key;
+    FMHA_VARIANT_REFERENCE_ORDER launches the plain heaviest-first table.
+    Both hold the same items, so O and LSE are equal bit for bit."""
+    import torch
+
+    prob = Problem(batch=b, nhead_q=h, seqlen_q=sq, causal=True, lse=True)
+    nq, nk, nlse = prob.sizes()
+    host = [torch.empty(n, dtype=torch.int16) for n in (nq, nk, nk, nq)]
+    p = build_params(prob, *host, torch.empty(nlse, dtype=torch.float32), None)
+    force = "pair" if form == "balanced_pair" else True
+    table, _ = fmha.balanced_plan(p, b, 1, 0, force=force)
+    plain, _ = fmha.balanced_plan(p, b, 1, 0, force=force, xccs=1)
+    print(f"{prob.name} {form}: {sum(x != y for x, y in zip(table, plain))} of {len(plain)} entries moved", flush=True)
+    assert table != plain and sorted(table) == sorted(plain)  # the device's 8 XCDs group this shape
+    v = fmha.VARIANTS[form]
+    q, k, vv = make_inputs(prob, "normal", 71, mult)
+    og, lg = run_kernel(prob, q, k, vv, variant=v)
+    op, lp = run_kernel(prob, q, k, vv, variant=v | fmha.VARIANT_REFERENCE_ORDER)
+    assert np.array_equal(og, op)
+    assert np.array_equal(lg, lp)
+
+
 def test_auto_takes_balanced_with_a_workspace_and_reuses_it():
     """B1 H2 S40000 causal: the automatic choice with a workspace is the
     balanced form (its bits equal the forced balanced launch's); a second

@@ -384,7 +384,7 @@ def test_balanced_plan_is_longest_first_over_every_key_tile(b, h, sq, sk, cus, f
     average work per resident block (two blocks per compute unit)."""
     p = valid_params(lse=False)
     p.nhead_q, p.nhead_k, p.seqlen_q, p.seqlen_k = h, h, sq, sk
-    items, sf = fmha.balanced_plan(p, b, 1, cus, force)
+    items, sf = fmha.balanced_plan(p, b, 1, cus, force, xccs=1)  # the plain order
     m_tiles = -(-sq // 128)
     n = [_ntiles(mt, sq, sk) for mt in range(m_tiles)]
     avg = sum(n) * h * b / (2 * cus)
@@ -413,7 +413,7 @@ def test_balanced_pair_plan_covers_every_pair_once(b, h, sq, sk, cus):
     the M-tile count; the workspace holds two partials per split M-tile."""
     p = valid_params(lse=False)
     p.nhead_q, p.nhead_k, p.seqlen_q, p.seqlen_k = h, h, sq, sk
-    items, sf = fmha.balanced_plan(p, b, 1, cus, "pair")
+    items, sf = fmha.balanced_plan(p, b, 1, cus, "pair", xccs=1)  # the plain order
     m_tiles = -(-sq // 128)
     units = (m_tiles + 1) // 2
     n = [_ntiles(min(2 * u + 1, m_tiles - 1), sq, sk) for u in range(units)]
@@ -429,6 +429,47 @@ def test_balanced_pair_plan_covers_every_pair_once(b, h, sq, sk, cus):
         ws = fmha.workspace_size(p, b, 1, fmha.VARIANT_BALANCED_PAIR)
         assert ws == (m_tiles - sf) * h * b * 2 * 4 * 34 * 64 * 4
 
+
+
+@pytest.mark.parametrize("b,h,sq,xccs,force,groups", [
+    (1, 2, 40000, 8, True, 4),     # cfg5: each (batch, head) on 4 XCDs
+    (1, 1, 40000, 8, True, 8),
+    (1, 4, 40000, 8, True, 2),
+    (1, 2, 40000, 8, "pair", 4),
+    (2, 1, 60000, 8, True, 4),
+    (1, 3, 40000, 8, True, 1),     # 3 does not divide 8: plain order
+    (1, 2, 40000, 1, True, 1),     # one XCD: plain order
+    (1, 8, 40000, 8, True, 1),     # one group: plain order
+])
+def test_balanced_plan_orders_runs_by_first_key(b, h, sq, xccs, force, groups):
+    """With nhead_q * batch dividing the XCD count into groups (entry z runs
+    on group z % groups), each run of `groups` consecutive entries holds the
+    plain heaviest-first table's same items (so the dispatch sees the same
+    work per run), ordered by the first key tile they read: whole M-tiles and
+    first halves (key 0) before second halves (key ceil(n/2)), ties in the
+    plain order.  Otherwise the table is the plain one."""
+    p = valid_params(lse=False)
+    p.nhead_q = p.nhead_k = h
+    p.seqlen_q = p.seqlen_k = sq
+    got, sf = fmha.balanced_plan(p, b, 1, 256, force, xccs=xccs)
+    plain, sf1 = fmha.balanced_plan(p, b, 1, 256, force, xccs=1)
+    assert sf == sf1 and len(got) == len(plain)
+    if groups == 1:
+        assert got == plain
+        return
+    pair = force == "pair"
+    m_tiles = -(-sq // 128)
+
+    def first_key(it):
+        u, half = it
+        n = _ntiles(min(2 * u + 1, m_tiles - 1) if pair else u, sq, sq)
+        return (n + 1) // 2 if half == 1 else 0
+
+    assert got != plain
+    for r in range(0, len(plain), groups):
+        run, want = got[r:r + groups], plain[r:r + groups]
+        assert sorted(run) == sorted(want)
+        assert run == sorted(want, key=lambda it: (first_key(it), want.index(it)))
 
 @pytest.mark.parametrize("b,h,sq,causal", [(4, 16, 2048, 0), (4, 16, 2048, 1), (1, 16, 8192, 1), (1, 4, 32768, 1)])
 def test_balanced_plan_only_where_the_heaviest_m_tile_outlasts_the_average(b, h, sq, causal):
