@@ -72,6 +72,11 @@ WORKLOADS = {
 }
 
 
+def _argv():
+    """This run's arguments, quoted for a shell."""
+    return " ".join(shlex.quote(a) for a in sys.argv[1:])
+
+
 def _bench(*args):
     return [sys.executable, os.path.join(ROOT, "bench.py"), *args]
 
@@ -187,12 +192,12 @@ def profile_forms(args):
 
     probs = baseline_problems()
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on " + ", ".join(args.forms.split(",")), "",
-          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof "
-          f"{' '.join(shlex.quote(a) for a in sys.argv[1:])}` on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
+          f"MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof {_argv()}` "
+          "on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
           "`auto` is the launcher's own choice. TFLOP/s use the repo FLOP convention "
           "(4·B·H·Sq·Sk·64, ×0.5 causal; varlen counts max(S) for every sequence, and the exact count of "
           "visible (q, k) pairs is given beside it).", ""]
-    fig = {"made_by": f"python -m fmha_native_amd.rocprof --forms {shlex.quote(args.forms)}", "forms": {}}
+    fig = {"made_by": f"python -m fmha_native_amd.rocprof {_argv()}", "forms": {}}
     # the counters' scale, from a device copy of known size (as the main run)
     copy = {}
     copy_cmds = []
@@ -305,7 +310,7 @@ def profile_short(args):
     """Short sequences through the bench CLI: kernel trace per shape and form."""
     shapes = [(m, 16384 // sq, sq) for m in (0, 1) for sq in (64, 128, 192, 256, 512)]
     md = ["# Short sequences: achieved HBM bandwidth (MI355X, one GPU)", "",
-          "Every figure from one run of `python -m fmha_native_amd.rocprof --short` on one box (repo root, "
+          f"Every figure from one run of `python -m fmha_native_amd.rocprof {_argv()}` on one box (repo root, "
           "`TMPDIR=/tmp`); each pass is its own process under `timeout -s KILL`:", "",
           "    rocprofv3 --kernel-trace --stats -d <out>/<tag> -o run -- fmha_native_amd/bench_fmha_fwd "
           "-b <B> -h 16 -s <S> --mask <0|1> --lse 1 --dist normal --warmup 5 --iters 100 --variant <auto|regular>",
@@ -404,10 +409,9 @@ def main():
         return
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on cfg2 (dense B4 H16 S2048) and cfg3 (causal B1 H16 "
           "S8192 + LSE)", "",
-          "MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof` on one box "
-          "(the passes below, from the repo root, each under `timeout -s KILL`).", ""]
-    fig = {"made_by": "python -m fmha_native_amd.rocprof" + (f" --json {os.path.relpath(args.json, ROOT)}"
-                                                             if args.json else "")}
+          f"MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof {_argv()}` "
+          "on one box (the passes below, from the repo root, each under `timeout -s KILL`).", ""]
+    fig = {"made_by": f"python -m fmha_native_amd.rocprof {_argv()}"}
 
     # 0. bench.py itself, unprofiled
     cmd = [sys.executable, os.path.join(ROOT, "bench.py"), "--steps", str(args.steps), "--warmup", "20",
