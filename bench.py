@@ -429,6 +429,9 @@ def main():
                          "(default: the launcher's choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run `steps` device-to-device copies of this many MiB (HBM counter calibration)")
+    ap.add_argument("--gemm-probe", type=int, default=0,
+                    help="only time `steps` bf16 N x N x N torch.matmul launches (the library GEMM beside the "
+                         "kernel on one box: MFMA rate and clock under the power cap)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards "
@@ -450,6 +453,30 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": args.steps}))
+        return
+    if args.gemm_probe:
+        n = args.gemm_probe
+        g = torch.Generator(device="cuda:0").manual_seed(42)
+        a = torch.randn(n, n, device="cuda:0", dtype=torch.float32, generator=g).to(torch.bfloat16)
+        b = torch.randn(n, n, device="cuda:0", dtype=torch.float32, generator=g).to(torch.bfloat16)
+        c = torch.empty(n, n, device="cuda:0", dtype=torch.bfloat16)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.3:  # bring the clock up, as time_problem does
+            for _ in range(10):
+                torch.matmul(a, b, out=c)
+            torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            torch.matmul(a, b, out=c)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            torch.matmul(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        print(json.dumps({"gemm_n": n, "dtype": "bf16", "steps": args.steps, "ms_per_gemm": round(ms, 5),
+                          "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)}))
         return
     cfg2, cfg3 = _problems()
     if args.only:

@@ -185,6 +185,55 @@ def _util_row(c, n_se=NUM_SE):
     return ghz, mfma_per_simd / active, mfma_per_simd / (c["dispatch_ns"] * 2.4)
 
 
+def profile_gemm(args):
+    """A bf16 library GEMM (torch.matmul, N x N x N) beside cfg2 and cfg3 on
+    one box: TFLOP/s from HIP events, and from one counter pass each the
+    active cycles, the clock they imply, MFMA busy and busy x clock, the
+    product the chip's power cap holds about constant across this kernel's
+    forms."""
+    n = args.gemm
+    md = [f"# MFMA rate under the power cap: bf16 GEMM {n}³ beside cfg2 and cfg3 (MI355X, one GPU)", "",
+          f"Every figure from one run of `python -m fmha_native_amd.rocprof {_argv()}` on one box (repo root; each "
+          "pass its own process under `timeout -s KILL`). The GEMM is `torch.matmul` on bf16 operands (the "
+          "library's kernel, hipBLASLt on this image); cfg2 and cfg3 run this library's automatic form.", ""]
+    runs = [("gemm", _bench("--gemm-probe", str(n), "--steps", "50", "--warmup", "5"), 2.0 * n ** 3),
+            ("cfg2", _bench("--only", "cfg2", "--steps", str(args.steps), "--warmup", "10"), WORKLOADS["cfg2"]["flops"]),
+            ("cfg3", _bench("--only", "cfg3", "--steps", str(args.steps // 2), "--warmup", "10"),
+             WORKLOADS["cfg3"]["flops"])]
+    rows, cmds = [], []
+    for tag, prog, flops in runs:
+        print(f"[rocprof] bench: {' '.join(prog)}", flush=True)
+        r = subprocess.run(["timeout", "-s", "KILL", "300", *prog], capture_output=True, text=True)
+        line = json.loads([l for l in r.stdout.splitlines() if l.startswith("{")][-1])
+        ms = line.get("ms_per_gemm") or line["ms_per_step"]
+        cmds.append(" ".join("python3" if c == sys.executable else shlex.quote(c) for c in prog).replace(ROOT + "/", ""))
+        db, _l, ucmd = _run(f"pmc_util_{tag}", ["--pmc", *UTIL_COUNTERS], prog, args.out, 180)
+        cmds.append(ucmd)
+        cs = _counters(db, kernel_prefix="" if tag == "gemm" else "fmha_fwd")
+        # the GEMM pass also runs the operands' fill kernels: take the kernel
+        # with the most time
+        kname = max(cs, key=lambda k: cs[k]["dispatch_ns"] * cs[k]["dispatches"])
+        c = cs[kname]
+        ghz, busy, frac = _util_row(c, _num_se(db))
+        rows.append((tag, kname, ms, flops / (ms * 1e-3) / 1e12, c, ghz, busy, frac))
+    md += ["| workload | kernel | ms per launch (events) | TFLOP/s | % of 2516.6 | active cycles | clock ≥ | "
+           "MFMA busy | busy × clock | VALU instr per MFMA |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for tag, kname, ms, tf, c, ghz, busy, frac in rows:
+        valu = c.get("SQ_INSTS_VALU", 0) / max(1.0, c.get("SQ_INSTS_MFMA", 0))
+        md.append(f"| {tag} | `{kname.split('(')[0][:60]}` | {ms:.4f} | {tf:.1f} | {100 * tf / PEAK_BF16_TFLOPS:.1f}% | "
+                  f"{c['SQ_BUSY_CYCLES'] / _num_se(db) / 1e3:.1f}k | {ghz:.3f} GHz | {100 * busy:.1f}% | "
+                  f"{busy * ghz:.3f} GHz | {valu:.2f} |")
+    md += ["", "Active cycles = SQ_BUSY_CYCLES / shader engines; clock ≥ active cycles over the dispatch's duration "
+               "in the counter pass; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the active cycles; busy × "
+               "clock is the MFMA rate in GHz-equivalents of a fully busy SIMD (2.4 GHz at 100 % would be the "
+               "2516.6 TFLOP/s peak). VALU instructions per MFMA count every VALU instruction the counter sees "
+               "(MFMA included).", "", "Commands:", ""] + [f"    {c}" for c in cmds] + [""]
+    path = args.summary or os.path.join(args.out, "gemm.md")
+    with open(path, "w") as f:
+        f.write("\n".join(md))
+    print("\n".join(md), flush=True)
+
+
 def profile_forms(args):
     """Kernel trace and utilisation counters of other workloads in the forms
     ``args.forms`` names ("cfg4:auto,cfg5:regular", ...)."""
@@ -399,10 +448,15 @@ def main():
     ap.add_argument("--forms", default=None,
                     help="profile these workload:form pairs instead (e.g. cfg4:auto,cfg5:auto,cfg5:regular)")
     ap.add_argument("--short", action="store_true", help="profile the short-sequence shapes and cfg1 instead")
+    ap.add_argument("--gemm", type=int, default=0,
+                    help="profile a bf16 N x N x N library GEMM beside cfg2 and cfg3 instead")
     args = ap.parse_args()
     os.makedirs(args.out, exist_ok=True)
     if args.short:
         profile_short(args)
+        return
+    if args.gemm:
+        profile_gemm(args)
         return
     if args.forms:
         profile_forms(args)
