@@ -440,6 +440,8 @@ def test_balanced_pair_plan_covers_every_pair_once(b, h, sq, sk, cus):
     (1, 3, 40000, 8, True, 1),     # 3 does not divide 8: plain order
     (1, 2, 40000, 1, True, 1),     # one XCD: plain order
     (1, 8, 40000, 8, True, 1),     # one group: plain order
+    (1, 2, 40000, 4, True, 2),     # a 4-XCD partition: 2 groups
+    (1, 4, 40000, 4, True, 1),     # a 4-XCD partition, 4 heads: plain order
 ])
 def test_balanced_plan_orders_runs_by_first_key(b, h, sq, xccs, force, groups):
     """With nhead_q * batch dividing the XCD count into groups (entry z runs
