@@ -113,3 +113,75 @@ def test_wide_random_sweep():
         if i % 100 == 99:
             print(f"wide sweep: {i + 1} shapes, {runs} launches, {len(failed)} failed", flush=True)
     assert not failed, failed[:20]
+
+
+def _draw_varlen_causal(i):
+    rng = np.random.default_rng(70000 + i)
+    hk = int(rng.choice([1, 2, 4]))
+    hq = hk * int(rng.choice([1, 2, 4]))
+    n = int(rng.integers(1, 41))
+    seqs = [int(x) for x in rng.integers(0, 1501, n)]
+    if rng.random() < 0.3:  # empty and one-token sequences
+        seqs[int(rng.integers(0, n))] = 0
+        seqs[int(rng.integers(0, n))] = 1
+    if sum(seqs) == 0:
+        seqs[0] = 1
+    return Problem(batch=0, nhead_q=hq, nhead_k=hk, seqlen_q=0, causal=True, lse=bool(rng.integers(0, 2)),
+                   varlen_seqs=tuple(seqs), name=f"vc{i}-n{n}-h{hq}k{hk}")
+
+
+def test_random_varlen_causal_orders_bitwise():
+    """Thirty random causal varlen batches (1-40 sequences of 0-1,500
+    tokens, GQA): the level order, the sequence order and the automatic
+    choice give O and LSE bit for bit equal to the reference's order (every
+    row is written: O starts as a NaN pattern); every fifth batch is also
+    checked against the oracle."""
+    import oracle
+    from oracle import verify
+
+    from harness import make_inputs, run_kernel
+
+    R, T, S = fmha.VARIANT_REFERENCE_ORDER, fmha.VARIANT_TILE_MAJOR_ORDER, fmha.VARIANT_SEQUENCE_ORDER
+    bad = []
+    for i in range(30):
+        prob = _draw_varlen_causal(i)
+        q, k, v = make_inputs(prob, "normal", 300 + i)
+        o0, l0 = run_kernel(prob, q, k, v, variant=fmha.VARIANT_REGULAR | R)
+        for name, var in (("level", fmha.VARIANT_REGULAR | T), ("sequence", fmha.VARIANT_REGULAR | S),
+                          ("auto", fmha.VARIANT_AUTO)):
+            o1, l1 = run_kernel(prob, q, k, v, variant=var)
+            if not np.array_equal(o0, o1) or (prob.lse and not np.array_equal(l0, l1)):
+                bad.append((prob.name, name))
+        if i % 5 == 0:
+            o_ref, lse_ref = oracle.run(prob, q, k, v, p_trunc=False)
+            ok = verify.baseline_rule(o_ref, verify.bf16_bits_to_f32(o0))["pass"]
+            if prob.lse:
+                ok = ok and verify.lse_rule(lse_ref, l0)["pass"]
+            if not ok:
+                bad.append((prob.name, "oracle"))
+        print(f"varlen orders: {prob.name} done, {len(bad)} mismatches so far", flush=True)
+    assert not bad, bad
+
+
+def test_random_balanced_xcd_order_bitwise():
+    """Ten random dense causal shapes whose nhead_q * batch divides the XCD
+    count (1, 2 or 4): the balanced and balanced pair forms with the default
+    (XCD-ordered) table equal the plain heaviest-first table bit for bit."""
+    from harness import make_inputs, run_kernel
+
+    bad = []
+    for i in range(10):
+        rng = np.random.default_rng(80000 + i)
+        hb = int(rng.choice([1, 2, 4]))
+        b = int(rng.choice([x for x in (1, 2, 4) if x <= hb]))
+        h = hb // b
+        s = int(rng.integers(2000, 24001))
+        prob = Problem(batch=b, nhead_q=h, nhead_k=h, seqlen_q=s, causal=True, lse=True, name=f"bx{i}-b{b}h{h}s{s}")
+        q, k, v = make_inputs(prob, "normal", 400 + i)
+        for var in (fmha.VARIANT_BALANCED, fmha.VARIANT_BALANCED_PAIR):
+            o0, l0 = run_kernel(prob, q, k, v, variant=var | fmha.VARIANT_REFERENCE_ORDER)
+            o1, l1 = run_kernel(prob, q, k, v, variant=var)
+            if not (np.array_equal(o0, o1) and np.array_equal(l0, l1)):
+                bad.append((prob.name, var))
+        print(f"balanced order: {prob.name} done", flush=True)
+    assert not bad, bad
