@@ -423,8 +423,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg1/cfg4/cfg5 side measurements")
-    ap.add_argument("--only", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
-                    help="time one workload only (profiling runs)")
+    ap.add_argument("--only", default=None,
+                    help="time one workload only (profiling runs): cfg1..cfg5, or a dense shape "
+                         "dense-B<b>H<h>S<s> / causal-B<b>H<h>S<s>")
     ap.add_argument("--variant", default="auto", help="with --only: the kernel form, optionally |reference, |tilemajor or |sequence "
                          "(default: the launcher's choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -480,9 +481,9 @@ def main():
         return
     cfg2, cfg3 = _problems()
     if args.only:
-        from fmha_native_amd.problem import baseline_problems
+        from fmha_native_amd.problem import workload
 
-        prob, mult = {"cfg2": (cfg2, 1.0), "cfg3": (cfg3, 1.0)}.get(args.only) or baseline_problems()[args.only]
+        prob, mult = {"cfg2": (cfg2, 1.0), "cfg3": (cfg3, 1.0)}.get(args.only) or workload(args.only)
         r = time_problem(prob, args.steps, args.warmup, torch, mult, fmha.variant_code(args.variant))
         # launch order, for a profiler's trace: ramp, warmup, steps timed back
         # to back, then as many under the reference's protocol

@@ -146,3 +146,22 @@ def baseline_problems(varlen_seed=42):
         "cfg5": (Problem(batch=1, nhead_q=2, seqlen_q=40000, causal=True, lse=True,
                          name="cfg5_B1H2S40000_causal_x2"), 2.0),
     }
+
+
+def workload(spec):
+    """(Problem, input multiplier) of a workload name: one of the five
+    benchmark configurations ("cfg1" .. "cfg5"), or a dense shape written
+    "dense-B<b>H<h>S<s>" / "causal-B<b>H<h>S<s>" (causal with LSE; N(0,1)
+    inputs)."""
+    import re
+
+    probs = baseline_problems()
+    if spec in probs:
+        return probs[spec]
+    m = re.fullmatch(r"(dense|causal)-B(\d+)H(\d+)S(\d+)", spec)
+    if not m:
+        raise ValueError(f"unknown workload {spec!r}: cfg1..cfg5, dense-B<b>H<h>S<s> or causal-B<b>H<h>S<s>")
+    causal = m.group(1) == "causal"
+    b, h, sq = (int(m.group(i)) for i in (2, 3, 4))
+    return Problem(batch=b, nhead_q=h, seqlen_q=sq, causal=causal, lse=causal, name=spec), 1.0
+

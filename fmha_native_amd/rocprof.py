@@ -237,9 +237,8 @@ def profile_gemm(args):
 def profile_forms(args):
     """Kernel trace and utilisation counters of other workloads in the forms
     ``args.forms`` names ("cfg4:auto,cfg5:regular", ...)."""
-    from fmha_native_amd.problem import baseline_problems
+    from fmha_native_amd.problem import workload
 
-    probs = baseline_problems()
     md = ["# rocprofv3 summary — fmha_fwd_d64_bf16 on " + ", ".join(args.forms.split(",")), "",
           f"MI355X (gfx950), one GPU, every figure from one run of `python -m fmha_native_amd.rocprof {_argv()}` "
           "on one box (the passes below, from the repo root, each under `timeout -s KILL`). "
@@ -260,7 +259,7 @@ def profile_forms(args):
     md += [f"    {c}" for c in copy_cmds] + [""]
     for spec in args.forms.split(","):
         wl, form = spec.split(":")
-        prob, _mult = probs[wl]
+        prob, _mult = workload(wl)
         tag = f"{wl}_{form}".replace("|", "-")
         steps = str(args.steps // 4 if wl != "cfg1" else args.steps)
         # unprofiled

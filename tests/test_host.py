@@ -271,3 +271,18 @@ def test_abtest_variants_and_specs():
                 Problem(**kw)
                 for v in case["variants"]:
                     abtest.parse_variant(v)
+
+
+def test_workload_names():
+    """bench.py --only and rocprof --forms take the five configurations or a
+    dense shape by name; anything else is refused."""
+    from fmha_native_amd.problem import workload
+
+    assert workload("cfg5")[1] == 2.0 and workload("cfg5")[0].seqlen_q == 40000
+    p, mult = workload("causal-B2H16S8192")
+    assert (p.batch, p.nhead_q, p.seqlen_q, p.causal, p.lse, mult) == (2, 16, 8192, True, True, 1.0)
+    p, _ = workload("dense-B1H16S4096")
+    assert (p.batch, p.nhead_q, p.seqlen_q, p.causal, p.lse) == (1, 16, 4096, False, False)
+    for bad in ("cfg6", "dense-B1H16", "causal-b1h2s3", ""):
+        with pytest.raises(ValueError):
+            workload(bad)
