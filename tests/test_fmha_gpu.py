@@ -412,6 +412,66 @@ def test_graph_capture_replays_match_eager():
         assert torch.equal(dl, l_ref), i
 
 
+@pytest.mark.parametrize("case", ["balanced", "balanced_pair", "pair_stream", "varlen_sequence_order"])
+def test_graph_capture_workspace_and_order_forms(case):
+    """The workspace forms (two launches: items, then the merge, with the
+    partials in the caller's workspace), the pair stream and the compact
+    varlen order allocate and memset nothing either: captured through
+    fmha_fwd_d64_bf16_ws, every replay (eager work and zeroed outputs between
+    replays) reproduces the eager result bit for bit."""
+    import torch
+
+    from harness import build_params, to_device
+
+    if case.startswith("balanced"):
+        p = Problem(batch=1, nhead_q=2, seqlen_q=12000, causal=True, lse=True)
+        var = fmha.VARIANTS[case]
+    elif case == "pair_stream":
+        p = Problem(batch=2, nhead_q=8, seqlen_q=2048, lse=True)
+        var = fmha.VARIANT_PAIR_STREAM
+    else:
+        p = Problem(batch=0, nhead_q=8, nhead_k=4, seqlen_q=0, causal=True, lse=True,
+                    varlen_seqs=(1000, 300, 2100, 0, 777))
+        var = fmha.VARIANT_REGULAR | fmha.VARIANT_SEQUENCE_ORDER
+    q, k, v = make_inputs(p, "normal", 31)
+    nq, nk, nlse = p.sizes()
+    dq, dk, dv = to_device(q, torch), to_device(k, torch), to_device(v, torch)
+    do = torch.zeros(nq, dtype=torch.int16, device="cuda:0")
+    dl = torch.zeros(nlse, dtype=torch.float32, device="cuda:0")
+    ss = p.seqstart()
+    dseq = torch.from_numpy(ss).to("cuda:0") if ss is not None else None
+    prm = build_params(p, dq, dk, dv, do, dl, dseq)
+    need = fmha.workspace_size(prm, p.batch, int(p.causal), var)
+    assert need >= 0
+    if case.startswith("balanced"):
+        assert need > 0
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda:0")
+    print("graph capture:", case, p.name, "workspace", need, flush=True)
+
+    def launch(stream):
+        fmha.fmha_fwd_d64_bf16_ws(prm, p.batch, int(p.causal), ws.data_ptr(), need, stream, var)
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        launch(s.cuda_stream)
+    torch.cuda.synchronize()
+    o_ref, l_ref = do.clone(), dl.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        launch(torch.cuda.current_stream().cuda_stream)
+    noise = torch.randn(1 << 20, device="cuda:0")
+    for i in range(3):
+        do.zero_()
+        dl.zero_()
+        ws.zero_()  # the partials are written before they are read
+        noise.mul_(1.0001)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(do, o_ref), (case, i)
+        assert torch.equal(dl, l_ref), (case, i)
+
+
 def test_concurrent_streams_independent():
     """Two launches in flight at once on two streams (different shapes and
     masks) give the same bits as each run alone: the launcher keeps no
