@@ -166,7 +166,8 @@ hipError_t fmha_fwd_d64_bf16(const FmhaFwdParams* params, int batch, int causal,
 #define FMHA_VARIANT_BALANCED_PAIR 7 /* fmha_fwd_d64_bf16_ws only: the balanced form over M-tile pairs */
 #define FMHA_VARIANT_PAIR_STREAM 8   /* dense layouts (not varlen): one pair block per compute unit looping
                                         over M-tile pairs (causal: a pair, then its mirror) */
-#define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid */
+#define FMHA_VARIANT_REFERENCE_ORDER 16 /* flag: batch after batch, on the (nhead_q, tiles, batch) grid;
+                                           balanced forms: the plain heaviest-first item table */
 #define FMHA_VARIANT_TILE_MAJOR_ORDER 32 /* flag: causal dense batches on the tile-major entries (any K/V
                                             size); causal varlen (regular form, <= 64 sequences): level order */
 #define FMHA_VARIANT_SEQUENCE_ORDER 64  /* flag: causal varlen (regular form, <= 64 sequences): sequence
@@ -198,7 +199,10 @@ hipError_t fmha_fwd_d64_bf16_variant(const FmhaFwdParams* params, int batch, int
  *            average work per unit are split; a group's partial goes to its
  *            own M-tile's slot, so the workspace size is the same formula),
  *            or any other variant (workspace unused, as
- *            fmha_fwd_d64_bf16_variant).
+ *            fmha_fwd_d64_bf16_variant).  The balanced forms order their
+ *            item table per group of XCDs when nhead_q * batch divides the
+ *            XCD count; FMHA_VARIANT_REFERENCE_ORDER OR-ed in keeps the plain
+ *            heaviest-first table (the same items: identical results).
  *   workspace: device memory, 256-byte aligned, at least
  *            fmha_fwd_d64_bf16_workspace_size() bytes, or NULL with 0 bytes
  *            (then never balanced).  Its contents need no initialisation;
